@@ -1,0 +1,149 @@
+#!/usr/bin/env python3
+"""Headline benchmark: fused f16 Matmul -> row-Softmax on one MI355X.
+
+Workload ("C2"): A[2048x1024] f16 x B[1024x2048] f16,
+f32 accumulation, softmax over N=2048, f16 output; inputs N(0,1)/sqrt(K)
+(synthetic, generated on the GPU).  A "step" is one call of the fused chain
+(`wtc_matmul_softmax`, one kernel launch on the exchange path).  Inputs are
+resident in HBM before timing starts; W untimed warmups, then K back-to-back
+timed steps bracketed by device synchronisation, timed with HIP events on the
+launch stream (the reference's own method, WelderProfiler.cpp:752-792).
+
+Prints ONE JSON line.  `roofline` prices the kernel against dense f16 MFMA
+peak (2.5 PFLOP/s); `traffic` comes from the committed rocprofv3 --pmc
+summary of this same command (profiles/), or is null.  `cpu_baseline` times
+the chain lowered to f32 loops (oracle/, the restatement of the reference's
+mlir-opt CPU path) on a bounded sample of rows on this host.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_F16_TFLOPS = 2500.0     # MI355X dense f16/bf16 MFMA
+PEAK_HBM_GBS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--path", default="auto", choices=["auto", "exchange", "split", "unfused"])
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="budget of the cpu_baseline sample (0 disables it)")
+    return ap.parse_args()
+
+
+def cpu_baseline(a_host, b_host, n, k, budget_s):
+    """f32 loops restatement of the reference CPU path on a bounded row sample."""
+    from oracle import oracle as O
+    threads = min(O.cpu_max_threads(), int(os.environ.get("OMP_NUM_THREADS", "16") or 16))
+    _, t1 = O.cpu_chain_loops(a_host, b_host, 0, threads, threads)  # calibration: one row per thread
+    per_row = max(t1 / 1.0, 1e-6)   # seconds per `threads` rows
+    rows = max(threads, int(budget_s / per_row) * threads)
+    rows = min(rows, a_host.shape[0])
+    _, secs = O.cpu_chain_loops(a_host, b_host, 0, rows, threads)
+    tflops = 2.0 * rows * n * k / secs / 1e12
+    return {"value": tflops, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"{rows} of 2048 rows of C2 (f32 i-j-k loops + max/exp/sum/div, "
+                      f"OpenMP over rows), {secs:.1f} s"}
+
+
+def load_traffic():
+    p = ROOT / "profiles" / "c2_f16_exchange_traffic.json"
+    if not p.exists():
+        return None
+    try:
+        return json.loads(p.read_text()).get("hbm_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); this build has no "
+              "multi-GPU path", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from welder_typical_chain_amd import _lib
+    from welder_typical_chain_amd.chain import matmul_softmax, new_workspace, workspace_size
+    from welder_typical_chain_amd.configs import HEADLINE as cfg
+
+    if not _lib.LIB_PATH.exists():
+        from welder_typical_chain_amd import build
+        build.build()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    m, n, k = cfg.m, cfg.n, cfg.k
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    a = (torch.randn((m, k), generator=g, device=dev) / math.sqrt(k)).to(torch.float16)
+    b = (torch.randn((k, n), generator=g, device=dev) / math.sqrt(k)).to(torch.float16)
+    out = torch.empty((m, n), dtype=torch.float16, device=dev)
+    ws = new_workspace(workspace_size(1, m, n, k, _lib.DTYPE_F16, _lib.DTYPE_F16, args.path), dev)
+
+    def step():
+        matmul_softmax(a, b, out=out, path=args.path, workspace=ws)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    t_host0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(args.steps):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    t_host = time.perf_counter() - t_host0
+    ms = e0.elapsed_time(e1) / args.steps
+    flops = cfg.flops
+    tflops = flops / (ms * 1e-3) / 1e12
+    from welder_typical_chain_amd.chain import read_error_flags
+    flags = read_error_flags(ws)
+    row_dev = float((out.float().sum(-1) - 1).abs().max())
+
+    cpu = None
+    if args.cpu_seconds > 0:
+        cpu = cpu_baseline(a.float().cpu().numpy(), b.float().cpu().numpy(), n, k, args.cpu_seconds)
+
+    line = {
+        "metric": "fused matmul+softmax TFLOP/s & % f16 MFMA peak (M=N=2048,K=1024)",
+        "value": round(tflops, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "us_per_call": ms * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic N(0,1)/sqrt(K) f16 generated on the GPU",
+        "config": {"workload": "C2 fused f16 matmul->row-softmax", "m": m, "n": n, "k": k,
+                   "batch": 1, "accumulate": "f32", "out_dtype": "f16", "path": args.path},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 3), "peak": PEAK_F16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tflops / PEAK_F16_TFLOPS, 4),
+                     "traffic": load_traffic()},
+        "cpu_baseline": cpu,
+        "checks": {"row_sum_max_dev": row_dev, "device_error_flags": flags,
+                   "host_wall_s_timed_region": round(t_host, 4)},
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

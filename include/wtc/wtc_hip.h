@@ -1,0 +1,96 @@
+/*
+ * wtc_hip.h -- launcher C-ABI of the MI355X (gfx950) fused Matmul->row-Softmax
+ * kernels:  out[b] = softmax_row(logit_scale * scale_a * scale_b * (A[b] . B[b])).
+ *
+ * Replaces the reference's launch boundary, which is the welder-profiler
+ * runtime: it text-parses `gpu.launch_func` lines of the NVVM artifact
+ * (backend/welder/compiler/solver/WelderProfilerParsing.h:211-282), binds
+ * memref descriptors (WelderProfilerRuntime.h:1-102), and launches with
+ * cuLaunchKernel (backend/welder/compiler/solver/WelderProfiler.cpp:752-792).
+ * A HIP code object has no such text form, so the launch is a C call taking
+ * device pointers.  All buffers are owned by the caller; the library owns
+ * only a per-device default workspace (used when `workspace` is NULL).
+ *
+ * Layouts are dense row-major: A [batch][m][k], B [batch][k][n],
+ * out [batch][m][n] (the reference's strides [K,1] / [N,1] / [N,1],
+ * bench/run_ab.sh:30-33).  Pointers must be 16-byte aligned; k*elem_bytes
+ * must be a multiple of 16 and n a multiple of 8.  m, n, batch may be 0
+ * (nothing to do); k may be 0 (every row is uniform 1/n).
+ *
+ * Thread safety: calls on one device that share a workspace (including the
+ * default one) must not overlap; pass distinct workspaces to run calls
+ * concurrently on several streams.
+ */
+#ifndef WTC_HIP_H
+#define WTC_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. */
+#define WTC_OK 0
+#define WTC_ERR_ARG 1          /* bad pointer, size, dtype or alignment */
+#define WTC_ERR_WORKSPACE 2    /* caller workspace too small */
+#define WTC_ERR_HIP 3          /* a HIP runtime call failed */
+#define WTC_ERR_UNSUPPORTED 4  /* shape / path combination not available */
+
+/* Element types. */
+#define WTC_DTYPE_F32 0
+#define WTC_DTYPE_F16 1
+#define WTC_DTYPE_BF16 2
+#define WTC_DTYPE_FP8_E4M3 3 /* OCP e4m3 ("fn"), inputs only */
+
+/* Execution paths. */
+#define WTC_PATH_AUTO 0      /* exchange when every tile is co-resident, else split */
+#define WTC_PATH_EXCHANGE 1  /* one kernel, row statistics exchanged between tiles */
+#define WTC_PATH_SPLIT 2     /* two kernels: tile pass + row rescale (online two-pass) */
+#define WTC_PATH_UNFUSED 3   /* five kernels: matmul, max, exp, sum, divide */
+
+/* The fused chain.  in_dtype is one of F32/F16/BF16/FP8_E4M3; out_dtype one of
+ * F32/F16/BF16.  scale_a / scale_b are the per-tensor dequantisation scales
+ * of fp8 inputs (pass 1 otherwise); logit_scale multiplies A.B before the
+ * softmax (1/sqrt(d) for attention scores).  `stream` is a hipStream_t
+ * (NULL = the null stream).  Asynchronous: returns after enqueueing. */
+int wtc_matmul_softmax(const void *a, const void *b, void *out, int64_t batch,
+                       int64_t m, int64_t n, int64_t k, int in_dtype,
+                       int out_dtype, float logit_scale, float scale_a,
+                       float scale_b, int path, void *workspace,
+                       size_t workspace_bytes, void *stream);
+
+/* Bytes of workspace wtc_matmul_softmax needs for this problem and path
+ * (AUTO, EXCHANGE and SPLIT need the same amount).  Negative on bad args. */
+int64_t wtc_matmul_softmax_workspace_size(int64_t batch, int64_t m, int64_t n,
+                                          int64_t k, int in_dtype,
+                                          int out_dtype, int path);
+
+/* Zero a caller workspace with a kernel on `stream` (required once, before
+ * its first use; safe inside graph capture). */
+int wtc_workspace_init(void *workspace, size_t workspace_bytes, void *stream);
+
+/* The launch plan for a device with `cu_count` compute units of which each
+ * holds `wg_per_cu` chain workgroups: grid size, chosen path and workspace
+ * bytes.  Pure host arithmetic (no GPU needed). */
+int wtc_plan(int64_t batch, int64_t m, int64_t n, int64_t k, int in_dtype,
+             int out_dtype, int path, int cu_count, int wg_per_cu,
+             int64_t *grid, int *chosen_path, int64_t *workspace_bytes);
+
+/* Reads (and with clear != 0, resets) the device error flags of a workspace
+ * (NULL = the default workspace of the current device).  Bit 0: a row-block
+ * wait of the exchange path timed out.  Synchronises the device. */
+int wtc_read_error_flags(void *workspace, uint32_t *flags, int clear);
+
+/* Message of the last failing call on this thread ("" if none). */
+const char *wtc_last_error(void);
+
+/* Library version string. */
+const char *wtc_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* WTC_HIP_H */

@@ -1,0 +1,208 @@
+// layout_check.cpp -- CPU replay of one workgroup of chain_tile_kernel.
+//
+// Uses the kernel's own index maps (welder_typical_chain_amd/csrc/tile_layout.h)
+// to move one k-tile of A and B from "HBM" through the register transpose into
+// the LDS stage, read the MFMA fragments back, run a reference model of the
+// 32x32xK MFMA (lane l supplies row/column l%32 and k-group l/32; register v of
+// the result holds D[8*(v/4) + 4*(l/32) + v%4][l%32]), and map the
+// accumulators to output coordinates the way the epilogue does.  Values are
+// small integers so the products are exact; the result must equal the plain
+// integer matmul.  Also checks that every LDS byte of the stage is written
+// exactly once, that the XCD remap is a bijection, and counts LDS bank
+// conflicts (64 banks x 4 bytes, 16 lanes per 128-bit access phase).
+//
+// Build: g++ -O2 -std=c++17 -I<csrc> layout_check.cpp; prints "OK" and exits 0.
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <set>
+#include <vector>
+
+#include "tile_layout.h"
+
+using namespace wtc;
+
+static int g_fail = 0;
+#define CHECK(c, ...)                           \
+  do {                                          \
+    if (!(c)) {                                 \
+      if (g_fail < 20) std::printf(__VA_ARGS__); \
+      ++g_fail;                                 \
+    }                                           \
+  } while (0)
+
+constexpr int BM = 128, BN = 128;
+
+struct Conflicts {
+  int worst = 1;
+  void phase(const std::vector<int>& addrs, int bytes_per_lane) {
+    // addrs: byte address per lane of one 16-lane phase
+    std::map<int, int> use;
+    for (int a : addrs)
+      for (int d = 0; d < bytes_per_lane / 4; ++d) use[((a / 4) + d) % 64]++;
+    for (auto& kv : use) worst = std::max(worst, kv.second);
+  }
+};
+
+static int64_t elem(const std::vector<uint8_t>& buf, size_t off, int sz) {
+  if (sz == 1) return buf[off];
+  if (sz == 2) { uint16_t x; std::memcpy(&x, buf.data() + off, 2); return x; }
+  uint32_t x; std::memcpy(&x, buf.data() + off, 4); return x;
+}
+
+static void run(int sz, const char* name) {
+  const int KE = kKTileBytes / sz;  // elements of K in one k-tile
+  const int EPC = kChunkBytes / sz;
+  // global tiles with small distinct-ish integer values
+  std::vector<uint8_t> A((size_t)BM * kKTileBytes), B((size_t)KE * BN * sz);
+  for (int m = 0; m < BM; ++m)
+    for (int k = 0; k < KE; ++k) {
+      uint32_t v = (uint32_t)((m * 7 + k * 3) % 13 + 1);
+      std::memcpy(A.data() + (size_t)m * kKTileBytes + k * sz, &v, sz);
+    }
+  for (int k = 0; k < KE; ++k)
+    for (int n = 0; n < BN; ++n) {
+      uint32_t v = (uint32_t)((k * 5 + n * 11) % 17 + 1);
+      std::memcpy(B.data() + ((size_t)k * BN + n) * sz, &v, sz);
+    }
+  const int A_STAGE = BM * kKTileBytes;
+  std::vector<uint8_t> lds((size_t)A_STAGE + BN * kKTileBytes, 0);
+  std::vector<int> cover(lds.size(), 0);
+  Conflicts cw_a, cw_b, cr_a, cr_b;
+
+  // ---- A: all 256 threads, 4 passes of one 16-byte chunk each
+  for (int j = 0; j < 4; ++j)
+    for (int wave = 0; wave < 4; ++wave)
+      for (int ph = 0; ph < 4; ++ph) {
+        std::vector<int> addrs;
+        for (int l = ph * 16; l < ph * 16 + 16; ++l) {
+          const int t = wave * 64 + l;
+          const int row = a_load_row(t, j), c = a_load_chunk(t);
+          const int off = a_lds_offset(row, c);
+          addrs.push_back(off);
+          std::memcpy(lds.data() + off, A.data() + (size_t)row * kKTileBytes + c * 16, 16);
+          for (int b = 0; b < 16; ++b) cover[off + b]++;
+        }
+        cw_a.phase(addrs, 16);
+      }
+  // ---- B: all 256 threads transpose an (EPC k) x 4 block into 4 chunks
+  for (int c = 0; c < 4; ++c)
+    for (int wave = 0; wave < 4; ++wave)
+      for (int ph = 0; ph < 4; ++ph) {
+        std::vector<int> addrs;
+        for (int l = ph * 16; l < ph * 16 + 16; ++l) {
+          const int t = wave * 64 + l;
+          const int g = b_load_colgroup(t), kc = b_load_chunkrow(t);
+          // the loader's k-rows as 16 row-major words, 4 columns per row
+          uint32_t words[16];
+          const int rows = EPC, row_bytes = 4 * sz;
+          for (int r = 0; r < rows; ++r)
+            std::memcpy(reinterpret_cast<uint8_t*>(words) + r * row_bytes,
+                        B.data() + ((size_t)(kc * EPC + r) * BN + 4 * g) * sz, row_bytes);
+          auto rw = [&](int i) { return words[i]; };
+          uint32_t unit[4];
+          for (int w = 0; w < 4; ++w) unit[w] = b_unit_word(rw, sz, c, w);
+          const int off = A_STAGE + b_lds_offset(kc, 4 * g + c, BN);
+          addrs.push_back(off);
+          std::memcpy(lds.data() + off, unit, 16);
+          for (int b = 0; b < 16; ++b) cover[off + b]++;
+        }
+        cw_b.phase(addrs, 16);
+      }
+  for (size_t i = 0; i < cover.size(); ++i)
+    CHECK(cover[i] == 1, "[%s] LDS byte %zu written %d times\n", name, i, cover[i]);
+
+  // ---- fragments + reference MFMA
+  std::vector<int64_t> acc(4 * 4 * 64 * 16, 0);  // [wave][mt*2+nt][lane][v]
+  auto ACC = [&](int wave, int mt, int nt, int l, int v) -> int64_t& {
+    return acc[(((size_t)wave * 4 + mt * 2 + nt) * 64 + l) * 16 + v];
+  };
+  const int steps = kChunksPerKTile / 2;  // chunk pairs per k-tile
+  for (int wave = 0; wave < 4; ++wave) {
+    const int wm = wave >> 1, wn = wave & 1;
+    for (int s = 0; s < steps; ++s) {
+      // operand bytes per lane: [lane][16]
+      std::vector<std::vector<uint8_t>> af(2, std::vector<uint8_t>(64 * 16)), bf(2, std::vector<uint8_t>(64 * 16));
+      for (int mt = 0; mt < 2; ++mt)
+        for (int ph = 0; ph < 4; ++ph) {
+          std::vector<int> addrs;
+          for (int l = ph * 16; l < ph * 16 + 16; ++l) {
+            const int off = a_lds_offset(wm * 64 + mt * 32 + frag_row(l), frag_chunk(l, s));
+            addrs.push_back(off);
+            std::memcpy(&af[mt][l * 16], lds.data() + off, 16);
+          }
+          cr_a.phase(addrs, 16);
+        }
+      for (int nt = 0; nt < 2; ++nt)
+        for (int ph = 0; ph < 4; ++ph) {
+          std::vector<int> addrs;
+          for (int l = ph * 16; l < ph * 16 + 16; ++l) {
+            const int off = A_STAGE + b_lds_offset(frag_chunk(l, s), wn * 64 + nt * 32 + frag_row(l), BN);
+            addrs.push_back(off);
+            std::memcpy(&bf[nt][l * 16], lds.data() + off, 16);
+          }
+          cr_b.phase(addrs, 16);
+        }
+      // D = X . Y with X = B^T fragment (rows i <- lane%32), Y = A^T fragment
+      for (int mt = 0; mt < 2; ++mt)
+        for (int nt = 0; nt < 2; ++nt) {
+          int64_t D[32][32] = {};
+          for (int i = 0; i < 32; ++i)
+            for (int j = 0; j < 32; ++j)
+              for (int g = 0; g < 2; ++g)
+                for (int e = 0; e < EPC; ++e)
+                  D[i][j] += elem(bf[nt], (size_t)(i + 32 * g) * 16 + e * sz, sz) *
+                             elem(af[mt], (size_t)(j + 32 * g) * 16 + e * sz, sz);
+          for (int l = 0; l < 64; ++l)
+            for (int v = 0; v < 16; ++v) ACC(wave, mt, nt, l, v) += D[acc_i(l, v)][acc_j(l)];
+        }
+    }
+  }
+  // ---- epilogue coordinates vs the plain matmul
+  std::vector<int> seen(BM * BN, 0);
+  for (int wave = 0; wave < 4; ++wave) {
+    const int wm = wave >> 1, wn = wave & 1;
+    for (int mt = 0; mt < 2; ++mt)
+      for (int nt = 0; nt < 2; ++nt)
+        for (int l = 0; l < 64; ++l)
+          for (int v = 0; v < 16; ++v) {
+            const int m = wm * 64 + mt * 32 + acc_j(l);
+            const int n = wn * 64 + nt * 32 + acc_i(l, v);
+            seen[m * BN + n]++;
+            int64_t ref = 0;
+            for (int k = 0; k < KE; ++k)
+              ref += elem(A, (size_t)m * kKTileBytes + k * sz, sz) * elem(B, ((size_t)k * BN + n) * sz, sz);
+            CHECK(ACC(wave, mt, nt, l, v) == ref, "[%s] C[%d][%d] = %lld, want %lld\n", name, m, n,
+                  (long long)ACC(wave, mt, nt, l, v), (long long)ref);
+            if ((v & 3) != 0)
+              CHECK(acc_i(l, v) == acc_i(l, v & ~3) + (v & 3), "[%s] staging run not contiguous\n", name);
+          }
+  }
+  for (int i = 0; i < BM * BN; ++i) CHECK(seen[i] == 1, "[%s] output %d covered %d times\n", name, i, seen[i]);
+  std::printf("[%s] lds bank-conflict ways: A write %d, B write %d, A read %d, B read %d\n", name,
+              cw_a.worst, cw_b.worst, cr_a.worst, cr_b.worst);
+  CHECK(cr_a.worst == 1 && cr_b.worst == 1, "[%s] fragment reads conflict\n", name);
+  CHECK(cw_a.worst == 1 && cw_b.worst == 1, "[%s] stage writes conflict\n", name);
+}
+
+int main() {
+  run(2, "f16/bf16");
+  run(1, "fp8");
+  run(4, "f32");
+  for (int64_t G : {256LL, 16384LL, 8LL, 100LL, 7LL, 2048LL}) {
+    std::set<int64_t> s;
+    for (int64_t b = 0; b < G; ++b) s.insert(xcd_remap(b, G));
+    CHECK((int64_t)s.size() == G && *s.begin() == 0 && *s.rbegin() == G - 1, "xcd_remap not a bijection for %lld\n",
+          (long long)G);
+    if (G % 8 == 0)
+      for (int64_t b = 0; b < G; ++b)
+        CHECK(xcd_remap(b, G) / (G / 8) == b % 8, "xcd_remap: tile of block %lld off its XCD\n", (long long)b);
+  }
+  if (g_fail) {
+    std::printf("FAILED (%d)\n", g_fail);
+    return 1;
+  }
+  std::printf("OK\n");
+  return 0;
+}

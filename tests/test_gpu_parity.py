@@ -1,0 +1,126 @@
+"""GPU parity of the HIP chain against the CPU oracle (through the C-ABI).
+
+Every case prints its name before touching the GPU.  Tolerances are the ones
+stated in tests/parity_util.py.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+from oracle import oracle as O  # noqa: E402
+from welder_typical_chain_amd.configs import CONFIGS, ChainConfig  # noqa: E402
+
+from .parity_util import check_row_sums, compare_rows, run_chain, sample_rows  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+needs_gpu = pytest.mark.skipif(not torch.cuda.is_available(), reason="no GPU")
+
+
+def _announce(msg: str) -> None:
+    print(f"\n[gpu-case] {msg}", flush=True)
+
+
+def _check(cfg: ChainConfig, inp: O.ChainInputs, out: torch.Tensor, rows, batches=(0,)):
+    out_np = out.float().cpu().numpy()
+    if out_np.ndim == 2:
+        out_np = out_np[None]
+    metrics = []
+    for bt in batches:
+        logits, probs = O.chain_rows(inp.a[bt], inp.b[bt], rows, inp.scale)
+        metrics.append(compare_rows(out_np[bt][rows], probs, logits, cfg.out_dtype,
+                                    label=f"{cfg.name} batch {bt}"))
+    check_row_sums(out, cfg.name)
+    return metrics
+
+
+@needs_gpu
+def test_c1_f32_full(native_lib):
+    cfg = CONFIGS["C1"]
+    _announce("C1 f32 128x128x128 all rows")
+    inp = O.make_inputs(cfg, seed=0)
+    for path in ("auto", "exchange", "split", "unfused"):
+        out = run_chain(inp, cfg.in_dtype, cfg.out_dtype, path=path)
+        _check(cfg, inp, out, np.arange(cfg.m))
+
+
+@needs_gpu
+@pytest.mark.parametrize("path", ["auto", "exchange", "split", "unfused"])
+def test_c2_f16_headline(native_lib, path):
+    cfg = CONFIGS["C2"]
+    _announce(f"C2 f16 2048x2048x1024 path={path}")
+    inp = O.make_inputs(cfg, seed=0)
+    out = run_chain(inp, cfg.in_dtype, cfg.out_dtype, path=path)
+    _check(cfg, inp, out, sample_rows(cfg.m, 48))
+    from welder_typical_chain_amd.chain import read_error_flags
+    assert read_error_flags() == 0
+
+
+@needs_gpu
+@pytest.mark.parametrize("in_dtype,out_dtype", [("f16", "f16"), ("bf16", "bf16"), ("f16", "f32"),
+                                                ("fp8", "f16"), ("f32", "f32"), ("bf16", "f16")])
+@pytest.mark.parametrize("path", ["exchange", "split"])
+def test_ragged_shapes(native_lib, in_dtype, out_dtype, path):
+    # M, N, K not multiples of the 128x128 tile / 128-byte k-tile
+    m, n = 200, 264
+    k = {"f16": 72, "bf16": 72, "f32": 36, "fp8": 80}[in_dtype]
+    dist = "xorshift_uniform" if in_dtype == "f32" else "normal"
+    cfg = ChainConfig("ragged", 1, m, n, k, in_dtype, out_dtype, dist, 0.3)
+    _announce(f"ragged {in_dtype}->{out_dtype} {m}x{n}x{k} path={path}")
+    inp = O.make_inputs(cfg, seed=3)
+    out = run_chain(inp, in_dtype, out_dtype, path=path)
+    _check(cfg, inp, out, np.arange(m))
+
+
+@needs_gpu
+def test_c3_batched_attention(native_lib):
+    cfg = CONFIGS["C3"]
+    _announce("C3 f16 batched 8x2048x2048x128 (batch subset)")
+    inp = O.make_inputs(cfg, seed=0, batch=8)
+    out = run_chain(inp, cfg.in_dtype, cfg.out_dtype, batched=True)
+    _check(cfg, inp, out, sample_rows(cfg.m, 8), batches=(0, 5, 7))
+
+
+@needs_gpu
+def test_c4_wide_rows_bf16(native_lib):
+    cfg = CONFIGS["C4"]
+    _announce("C4 bf16 1024x32768x4096 split-N")
+    inp = O.make_inputs(cfg, seed=0)
+    out = run_chain(inp, cfg.in_dtype, cfg.out_dtype)
+    _check(cfg, inp, out, sample_rows(cfg.m, 4))
+
+
+@needs_gpu
+def test_c5_fp8(native_lib):
+    cfg = CONFIGS["C5"]
+    _announce("C5 fp8 8192x8192x4096")
+    inp = O.make_inputs(cfg, seed=0)
+    out = run_chain(inp, cfg.in_dtype, cfg.out_dtype)
+    _check(cfg, inp, out, sample_rows(cfg.m, 6))
+
+
+@needs_gpu
+def test_edge_k0_uniform(native_lib):
+    from welder_typical_chain_amd.chain import matmul_softmax
+    _announce("K=0 gives uniform rows; M=0 is a no-op")
+    a = torch.empty((130, 0), dtype=torch.float16, device="cuda")
+    b = torch.empty((0, 136), dtype=torch.float16, device="cuda")
+    for path in ("exchange", "split", "unfused"):
+        out = matmul_softmax(a, b, path=path)
+        torch.cuda.synchronize()
+        assert torch.allclose(out.float(), torch.full_like(out.float(), 1.0 / 136), rtol=1e-3, atol=0)
+    empty = matmul_softmax(torch.empty((0, 16), dtype=torch.float16, device="cuda"),
+                           torch.empty((16, 64), dtype=torch.float16, device="cuda"))
+    assert empty.shape == (0, 64)
+
+
+@needs_gpu
+def test_negative_scale_and_shift_invariance(native_lib):
+    _announce("negative logit scale; row shift invariance")
+    cfg = ChainConfig("neg", 1, 128, 256, 64, "f16", "f32", "normal", 0.5, logit_scale=-0.7)
+    inp = O.make_inputs(cfg, seed=11)
+    out = run_chain(inp, "f16", "f32")
+    _check(cfg, inp, out, np.arange(128))

@@ -1,0 +1,95 @@
+"""ctypes binding of ``libwtc_hip.so`` (the C-ABI in ``include/wtc/``).
+
+Loading fails loudly: there is no CPU or PyTorch fallback for any entry
+point.  Build the library first (``python -m welder_typical_chain_amd.build``).
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libwtc_hip.so"
+
+WTC_OK = 0
+WTC_ERR_ARG = 1
+WTC_ERR_WORKSPACE = 2
+WTC_ERR_HIP = 3
+WTC_ERR_UNSUPPORTED = 4
+
+DTYPE_F32 = 0
+DTYPE_F16 = 1
+DTYPE_BF16 = 2
+DTYPE_FP8_E4M3 = 3
+
+PATH_AUTO = 0
+PATH_EXCHANGE = 1
+PATH_SPLIT = 2
+PATH_UNFUSED = 3
+
+PATHS = {"auto": PATH_AUTO, "exchange": PATH_EXCHANGE, "split": PATH_SPLIT,
+         "unfused": PATH_UNFUSED}
+
+_c_i64 = ctypes.c_int64
+_c_p = ctypes.c_void_p
+
+# name -> (restype, argtypes); every symbol the headers under include/wtc declare.
+SIGNATURES = {
+    "wtc_matmul_softmax": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64,
+                                          ctypes.c_int, ctypes.c_int, ctypes.c_float,
+                                          ctypes.c_float, ctypes.c_float, ctypes.c_int,
+                                          _c_p, ctypes.c_size_t, _c_p]),
+    "wtc_matmul_softmax_workspace_size": (_c_i64, [_c_i64, _c_i64, _c_i64, _c_i64,
+                                                   ctypes.c_int, ctypes.c_int, ctypes.c_int]),
+    "wtc_workspace_init": (ctypes.c_int, [_c_p, ctypes.c_size_t, _c_p]),
+    "wtc_plan": (ctypes.c_int, [_c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_int, ctypes.c_int,
+                                ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                ctypes.POINTER(_c_i64), ctypes.POINTER(ctypes.c_int),
+                                ctypes.POINTER(_c_i64)]),
+    "wtc_read_error_flags": (ctypes.c_int, [_c_p, ctypes.POINTER(ctypes.c_uint32), ctypes.c_int]),
+    "wtc_last_error": (ctypes.c_char_p, []),
+    "wtc_version": (ctypes.c_char_p, []),
+    "welder_compile_typical_chain_to_nvvm": (ctypes.c_int, [
+        ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p,
+        _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_int, ctypes.c_int,
+        ctypes.c_char_p, ctypes.c_size_t]),
+    "welder_compile_typical_chain_to_hip": (ctypes.c_int, [
+        ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p,
+        _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_int, ctypes.c_int,
+        ctypes.c_char_p, ctypes.c_size_t]),
+    "welder_solver_solve_typical_chain": (ctypes.c_int, [
+        ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, _c_i64, ctypes.c_int,
+        ctypes.POINTER(_c_i64), ctypes.POINTER(_c_i64), ctypes.POINTER(_c_i64),
+        ctypes.POINTER(_c_i64), ctypes.POINTER(_c_i64), ctypes.c_char_p, ctypes.c_size_t]),
+}
+
+_lib = None
+
+
+class WtcError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"wtc error {code}: {msg}")
+        self.code = code
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library with every declared signature bound."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: the HIP extension is not built "
+                "(run python -m welder_typical_chain_amd.build); no fallback exists")
+        h = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(h, name, None)
+            if fn is None:
+                continue
+            fn.restype = res
+            fn.argtypes = args
+        _lib = h
+    return _lib
+
+
+def check(code: int) -> None:
+    if code != WTC_OK:
+        raise WtcError(code, lib().wtc_last_error().decode())

@@ -1,0 +1,103 @@
+"""PyTorch-facing entry point of the fused chain.
+
+PyTorch supplies device memory and the current HIP stream; every byte of the
+chain is computed by the HIP kernels behind ``wtc_matmul_softmax``.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+_IN_DTYPES = {
+    torch.float32: _lib.DTYPE_F32,
+    torch.float16: _lib.DTYPE_F16,
+    torch.bfloat16: _lib.DTYPE_BF16,
+    torch.float8_e4m3fn: _lib.DTYPE_FP8_E4M3,
+}
+_OUT_DTYPES = {
+    torch.float32: _lib.DTYPE_F32,
+    torch.float16: _lib.DTYPE_F16,
+    torch.bfloat16: _lib.DTYPE_BF16,
+}
+
+
+def _code_of(t: torch.Tensor) -> int:
+    if t.dtype == torch.uint8:  # raw e4m3 bytes
+        return _lib.DTYPE_FP8_E4M3
+    try:
+        return _IN_DTYPES[t.dtype]
+    except KeyError:
+        raise TypeError(f"unsupported input dtype {t.dtype}") from None
+
+
+def workspace_size(batch: int, m: int, n: int, k: int, in_dtype: int, out_dtype: int,
+                   path: str = "auto") -> int:
+    size = _lib.lib().wtc_matmul_softmax_workspace_size(batch, m, n, k, in_dtype, out_dtype,
+                                                        _lib.PATHS[path])
+    if size < 0:
+        _lib.check(_lib.WTC_ERR_ARG)
+    return int(size)
+
+
+def new_workspace(nbytes: int, device: torch.device | str = "cuda") -> torch.Tensor:
+    """A zero-initialised workspace buffer (256-byte aligned by the allocator)."""
+    ws = torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+    stream = torch.cuda.current_stream(ws.device).cuda_stream
+    _lib.check(_lib.lib().wtc_workspace_init(ws.data_ptr(), ws.numel(), stream))
+    return ws
+
+
+def matmul_softmax(a: torch.Tensor, b: torch.Tensor, *, out: torch.Tensor | None = None,
+                   out_dtype: torch.dtype | None = None, logit_scale: float = 1.0,
+                   scale_a: float = 1.0, scale_b: float = 1.0, path: str = "auto",
+                   workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """out = softmax_row(logit_scale * scale_a * scale_b * (a @ b)).
+
+    a: [M, K] or [batch, M, K]; b: [K, N] or [batch, K, N]; contiguous CUDA
+    tensors of float32 / float16 / bfloat16 / float8_e4m3fn (or uint8 holding
+    e4m3 bytes).  Runs on the current stream of a's device.
+    """
+    if a.dim() not in (2, 3) or b.dim() != a.dim():
+        raise ValueError("a and b must both be 2-D or both 3-D")
+    if not (a.is_cuda and b.is_cuda):
+        raise ValueError("inputs must be on the GPU")
+    if not (a.is_contiguous() and b.is_contiguous()):
+        raise ValueError("inputs must be contiguous")
+    batched = a.dim() == 3
+    batch = a.shape[0] if batched else 1
+    m, k = a.shape[-2:]
+    k2, n = b.shape[-2:]
+    if k != k2 or (batched and b.shape[0] != batch):
+        raise ValueError(f"shape mismatch: a {tuple(a.shape)} b {tuple(b.shape)}")
+    in_code = _code_of(a)
+    if _code_of(b) != in_code:
+        raise TypeError("a and b must have the same element type")
+    if out_dtype is None:
+        out_dtype = out.dtype if out is not None else (
+            torch.float32 if in_code == _lib.DTYPE_F32 else torch.float16)
+    out_code = _OUT_DTYPES[out_dtype]
+    shape = (batch, m, n) if batched else (m, n)
+    if out is None:
+        out = torch.empty(shape, dtype=out_dtype, device=a.device)
+    elif tuple(out.shape) != shape or out.dtype != out_dtype or not out.is_contiguous():
+        raise ValueError("out has the wrong shape, dtype or layout")
+    ws_ptr, ws_bytes = None, 0
+    if workspace is not None:
+        ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
+    stream = torch.cuda.current_stream(a.device).cuda_stream
+    with torch.cuda.device(a.device):
+        rc = _lib.lib().wtc_matmul_softmax(
+            a.data_ptr(), b.data_ptr(), out.data_ptr(), batch, m, n, k, in_code, out_code,
+            float(logit_scale), float(scale_a), float(scale_b), _lib.PATHS[path], ws_ptr,
+            ws_bytes, stream)
+    _lib.check(rc)
+    return out
+
+
+def read_error_flags(workspace: torch.Tensor | None = None, clear: bool = True) -> int:
+    import ctypes
+    flags = ctypes.c_uint32(0)
+    ptr = workspace.data_ptr() if workspace is not None else None
+    _lib.check(_lib.lib().wtc_read_error_flags(ptr, ctypes.byref(flags), int(clear)))
+    return int(flags.value)

@@ -1,0 +1,630 @@
+// fused_matmul_softmax.hip -- the Welder typical chain's hot path on gfx950:
+//   out[b, M, N] = softmax_row(scale * (A[b, M, K] . B[b, K, N]))
+// hand-written for CDNA4 (wave64, 32x32 MFMA, 160 KB LDS, 8 XCDs).
+//
+// Replaces the fused kernel that welder-compiler's GPU codegen emits
+// (reference: bench/baselines/default/fused/04c.after_linalg_to_loops.mlir:41-313,
+// chain spec mlir/matmul_softmax_chain_f16_native.mlir:7-95).
+//
+// One workgroup (256 threads = 4 waves in a 2x2 grid) owns a 128x128 output
+// tile.  Main loop: the A and B k-tiles (128 bytes of K each) are fetched
+// with buffer loads whose out-of-range lanes read zero (no branches, so the
+// outstanding-load count stays exact), `PF` k-tiles ahead of use; B arrives
+// N-contiguous and is transposed in registers; both go to a two-stage LDS ring, and every wave
+// runs a 64x64 block of 32x32 MFMAs with f32 accumulation.  The MFMA is issued
+// as D = B^T . A^T so that each lane's accumulators belong to ONE output row:
+// row max / sum are then in-register, one cross-half swap, and one LDS
+// exchange between the two waves sharing the row.
+//
+// Epilogues (template parameter EPI):
+//   kEpiExchange  single pass.  Every tile publishes its per-row (max, sumexp)
+//                 to HBM, the tiles of one row block (all co-resident, the
+//                 launcher checks occupancy) meet at a counter, each merges the
+//                 row statistics and writes normalised outputs once.
+//   kEpiSplit     first pass of the two-pass online softmax for rows wider
+//                 than what can be co-resident: stores exp2(y - tile_max) and
+//                 the per-tile (max, sumexp); `rescale_rows_kernel` merges the
+//                 statistics and rescales in place.
+//   kEpiLogits    stores scale*(A.B) in the output type (first kernel of the
+//                 unfused five-kernel baseline).
+//
+// Note on bit casts: `__builtin_bit_cast(float, vec[e])` applied directly to
+// an element of an ext_vector miscompiles with this toolchain (element 0 is
+// read for every e); elements are always copied to a scalar first.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "tile_layout.h"
+#include "wtc_kernels.h"
+
+namespace wtc {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int BM = 128;
+constexpr int BN = 128;
+constexpr int NTHREADS = 256;
+constexpr int A_STAGE_BYTES = BM * kKTileBytes;                  // 16 KiB
+constexpr int STAGE_BYTES = A_STAGE_BYTES + BN * kKTileBytes;    // 32 KiB
+constexpr int RING_BYTES = 2 * STAGE_BYTES;                      // 64 KiB
+constexpr uint32_t kOutOfRange = 0x80000000u;  // buffer offset that reads 0
+
+template <int OUT_DT> struct OutTraits;
+template <> struct OutTraits<DT_F32> { static constexpr int SZ = 4; };
+template <> struct OutTraits<DT_F16> { static constexpr int SZ = 2; };
+template <> struct OutTraits<DT_BF16> { static constexpr int SZ = 2; };
+
+template <int OUT_DT> struct EpiLayout {
+  static constexpr int PITCH = BN * OutTraits<OUT_DT>::SZ + 16;  // staging row pitch
+  static constexpr int STAGING = BM * PITCH;
+  static constexpr int UNION = STAGING > RING_BYTES ? STAGING : RING_BYTES;
+  static constexpr int RED_OFF = (UNION + 255) / 256 * 256;
+  // redmax[2][BM], redsum[2][BM], factor[BM]  (floats)
+  static constexpr int TOTAL = RED_OFF + 5 * BM * 4;
+};
+
+__device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+__device__ inline u32x4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+__device__ inline u32x2 bload8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0));
+}
+
+// -------------------------------------------------------------------------
+// HBM -> registers -> LDS staging of one k-tile.  Every thread issues the same
+// straight-line sequence: 4 x 128-bit loads of A and one B block (8 x 64-bit
+// for 16-bit types, 16 x 32-bit for fp8, 4 x 128-bit for f32).
+// -------------------------------------------------------------------------
+struct Tile {
+  __amdgpu_buffer_rsrc_t ra, rb;
+  int64_t row0, n0, M, N, K, lda, ldb;
+};
+
+__device__ inline uint32_t bload4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
+}
+
+template <int IN_DT> struct StageRegs {
+  u32x4 a[4];
+  uint32_t b[16];  // the thread's B k-rows, row-major, 4 columns per row
+
+  __device__ inline void load(const Tile& tl, int kt, int t) {
+    constexpr int SZ = dtype_bytes(IN_DT);
+    constexpr int EPC = kChunkBytes / SZ;
+    const int64_t kb = (int64_t)kt * kKTileBytes + a_load_chunk(t) * kChunkBytes;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t row = tl.row0 + a_load_row(t, j);
+      const bool ok = row < tl.M && kb < tl.K * SZ;
+      a[j] = bload16(tl.ra, ok ? (uint32_t)(row * tl.lda + kb) : kOutOfRange);
+    }
+    const int64_t n = tl.n0 + 4 * b_load_colgroup(t);
+    const int64_t k0 = (int64_t)kt * (kKTileBytes / SZ) + b_load_chunkrow(t) * EPC;
+#pragma unroll
+    for (int r = 0; r < EPC; ++r) {
+      const int64_t k = k0 + r;
+      const bool ok = n < tl.N && k < tl.K;
+      const uint32_t off = ok ? (uint32_t)(k * tl.ldb + n * SZ) : kOutOfRange;
+      if constexpr (SZ == 2) {
+        const u32x2 x = bload8(tl.rb, off);
+        b[2 * r] = x[0];
+        b[2 * r + 1] = x[1];
+      } else if constexpr (SZ == 1) {
+        b[r] = bload4(tl.rb, off);
+      } else {
+        const u32x4 x = bload16(tl.rb, off);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) b[4 * r + e] = x[e];
+      }
+    }
+  }
+
+  __device__ inline void store(uint8_t* stage, int t) const {
+    constexpr int SZ = dtype_bytes(IN_DT);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      *reinterpret_cast<u32x4*>(stage + a_lds_offset(a_load_row(t, j), a_load_chunk(t))) = a[j];
+    const int g = b_load_colgroup(t), kc = b_load_chunkrow(t);
+    uint8_t* sB = stage + A_STAGE_BYTES;
+    auto rw = [this](int i) { return b[i]; };
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      u32x4 v;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) v[w] = b_unit_word(rw, SZ, c, w);
+      *reinterpret_cast<u32x4*>(sB + b_lds_offset(kc, 4 * g + c, BN)) = v;
+    }
+  }
+};
+
+// -------------------------------------------------------------------------
+// MFMA over one LDS stage: wave (wm, wn) accumulates its 64x64 block.
+// acc[mt][nt] holds D = B^T A^T for m-subtile mt, n-subtile nt.
+// Fragments of step s+1 are read while the MFMAs of step s issue.
+// -------------------------------------------------------------------------
+struct Frags {
+  u32x4 a[2], b[2];
+};
+
+__device__ inline void read_frags(const uint8_t* stage, int lane, int wm, int wn, int s, Frags& f) {
+  const uint8_t* sA = stage;
+  const uint8_t* sB = stage + A_STAGE_BYTES;
+  const int r = frag_row(lane);
+  const int kch = frag_chunk(lane, s);
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+    f.a[mt] = *reinterpret_cast<const u32x4*>(sA + a_lds_offset(wm * 64 + mt * 32 + r, kch));
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt)
+    f.b[nt] = *reinterpret_cast<const u32x4*>(sB + b_lds_offset(kch, wn * 64 + nt * 32 + r, BN));
+}
+
+template <int IN_DT>
+__device__ inline void mma_step(const Frags& f, f32x16 (&acc)[2][2]) {
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      if constexpr (IN_DT == DT_F16) {
+        acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+            __builtin_bit_cast(f16x8, f.b[nt]), __builtin_bit_cast(f16x8, f.a[mt]), acc[mt][nt], 0, 0, 0);
+      } else if constexpr (IN_DT == DT_BF16) {
+        acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+            __builtin_bit_cast(bf16x8, f.b[nt]), __builtin_bit_cast(bf16x8, f.a[mt]), acc[mt][nt], 0, 0, 0);
+      } else {
+        const u32x4 bv = f.b[nt], av = f.a[mt];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t bw = bv[e], aw = av[e];
+          acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x2f32(
+              __builtin_bit_cast(float, bw), __builtin_bit_cast(float, aw), acc[mt][nt], 0, 0, 0);
+        }
+      }
+    }
+}
+
+__device__ inline void mma_step_fp8(const Frags& f0, const Frags& f1, f32x16 (&acc)[2][2]) {
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      const u32x4 a0 = f0.a[mt], a1 = f1.a[mt], b0 = f0.b[nt], b1 = f1.b[nt];
+      const i32x8 av = {(int)a0[0], (int)a0[1], (int)a0[2], (int)a0[3],
+                        (int)a1[0], (int)a1[1], (int)a1[2], (int)a1[3]};
+      const i32x8 bv = {(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3],
+                        (int)b1[0], (int)b1[1], (int)b1[2], (int)b1[3]};
+      acc[mt][nt] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bv, av, acc[mt][nt], 0, 0, 0, 0, 0, 0);
+    }
+}
+
+template <int IN_DT>
+__device__ inline void mma_stage(const uint8_t* stage, int lane, int wm, int wn,
+                                 f32x16 (&acc)[2][2]) {
+  constexpr int S = kChunksPerKTile / 2;  // chunk-pair steps per k-tile
+  Frags f[2];
+  read_frags(stage, lane, wm, wn, 0, f[0]);
+  if constexpr (IN_DT == DT_FP8) {
+#pragma unroll
+    for (int s = 0; s < S; s += 2) {
+      read_frags(stage, lane, wm, wn, s + 1, f[1]);
+      const Frags cur = f[0];
+      if (s + 2 < S) read_frags(stage, lane, wm, wn, s + 2, f[0]);
+      mma_step_fp8(cur, f[1], acc);
+    }
+  } else {
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      if (s + 1 < S) read_frags(stage, lane, wm, wn, s + 1, f[(s + 1) & 1]);
+      mma_step<IN_DT>(f[s & 1], acc);
+    }
+  }
+}
+
+// -------------------------------------------------------------------------
+// Output conversion
+// -------------------------------------------------------------------------
+template <int OUT_DT> __device__ inline void store4(uint8_t* dst, float x0, float x1,
+                                                    float x2, float x3);
+template <> __device__ inline void store4<DT_F32>(uint8_t* dst, float x0, float x1,
+                                                  float x2, float x3) {
+  u32x4 u = {__builtin_bit_cast(uint32_t, x0), __builtin_bit_cast(uint32_t, x1),
+             __builtin_bit_cast(uint32_t, x2), __builtin_bit_cast(uint32_t, x3)};
+  *reinterpret_cast<u32x4*>(dst) = u;
+}
+template <> __device__ inline void store4<DT_F16>(uint8_t* dst, float x0, float x1,
+                                                  float x2, float x3) {
+  const _Float16 h0 = (_Float16)x0, h1 = (_Float16)x1, h2 = (_Float16)x2, h3 = (_Float16)x3;
+  u32x2 u = {(uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16),
+             (uint32_t)__builtin_bit_cast(uint16_t, h2) | ((uint32_t)__builtin_bit_cast(uint16_t, h3) << 16)};
+  *reinterpret_cast<u32x2*>(dst) = u;
+}
+template <> __device__ inline void store4<DT_BF16>(uint8_t* dst, float x0, float x1,
+                                                   float x2, float x3) {
+  const __bf16 h0 = (__bf16)x0, h1 = (__bf16)x1, h2 = (__bf16)x2, h3 = (__bf16)x3;
+  u32x2 u = {(uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16),
+             (uint32_t)__builtin_bit_cast(uint16_t, h2) | ((uint32_t)__builtin_bit_cast(uint16_t, h3) << 16)};
+  *reinterpret_cast<u32x2*>(dst) = u;
+}
+
+__device__ inline float wave_xor32_max(float x) { return fmaxf(x, __shfl_xor(x, 32)); }
+__device__ inline float wave_xor32_sum(float x) { return x + __shfl_xor(x, 32); }
+
+// 64-bit relaxed atomic access at agent scope for the row statistics.
+__device__ inline void store_stat(float2* p, float m, float s) {
+  const uint64_t u = (uint64_t)__builtin_bit_cast(uint32_t, m) |
+                     ((uint64_t)__builtin_bit_cast(uint32_t, s) << 32);
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline float2 load_stat(const float2* p) {
+  const uint64_t u = __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+  const uint32_t lo = (uint32_t)u, hi = (uint32_t)(u >> 32);
+  return make_float2(__builtin_bit_cast(float, lo), __builtin_bit_cast(float, hi));
+}
+
+// Arrival of one tile at its row block's counter (called by one thread after
+// the tile's statistics are stored and released).  Returns once every tile
+// of the row block has arrived, or after spin_ticks of the 100 MHz clock (then
+// err gets bit 0 and the tile goes on with what it sees, so the kernel always
+// drains).  The last arriver resets the counter and bumps the generation
+// word, so the protocol keeps no per-launch state and survives graph replay.
+// The poll itself is a relaxed load: no cache maintenance inside the loop.
+__device__ inline void rowblock_barrier(uint32_t* cnt_gen, int nT, uint32_t* err,
+                                        uint64_t spin_ticks) {
+  uint32_t* cnt = cnt_gen;
+  uint32_t* gen = cnt_gen + 1;
+  const uint32_t g0 = __hip_atomic_load(gen, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
+  const uint32_t old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+  if (old == (uint32_t)(nT - 1)) {
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "agent");
+    __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_fetch_add(gen, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
+  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+  while (__hip_atomic_load(gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == g0) {
+    __builtin_amdgcn_s_sleep(2);
+    if (__builtin_amdgcn_s_memrealtime() - t0 > spin_ticks) {
+      __hip_atomic_fetch_or(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      break;
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+}
+
+// -------------------------------------------------------------------------
+// The kernel
+// -------------------------------------------------------------------------
+template <int IN_DT, int OUT_DT, int EPI, int PF>
+__global__ void __launch_bounds__(NTHREADS, 1)
+chain_tile_kernel(const ChainParams p) {
+  using L = EpiLayout<OUT_DT>;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[L::TOTAL];
+  float* redmax = reinterpret_cast<float*>(smem + L::RED_OFF);
+  float* redsum = redmax + 2 * BM;
+  float* factor = redsum + 2 * BM;
+
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = t >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  const int64_t tile = xcd_remap(blockIdx.x, gridDim.x);
+  const int64_t nt = tile % p.nT;
+  const int64_t rbg = tile / p.nT;  // row block across batches
+  const int64_t bt = rbg / p.nRB;
+  const int64_t rb = rbg % p.nRB;
+  const int64_t row0 = rb * BM;
+  const int64_t n0 = nt * BN;
+
+  constexpr int SZ = dtype_bytes(IN_DT);
+  Tile tl;
+  tl.ra = make_rsrc(p.a + bt * p.a_bstride, (uint32_t)p.a_bstride);
+  tl.rb = make_rsrc(p.b + bt * p.b_bstride, (uint32_t)p.b_bstride);
+  tl.row0 = row0;
+  tl.n0 = n0;
+  tl.M = p.M;
+  tl.N = p.N;
+  tl.K = p.K;
+  tl.lda = p.lda_bytes;
+  tl.ldb = p.ldb_bytes;
+  uint8_t* o_base = p.out + bt * p.o_bstride;
+  const int nk = (int)((p.K * SZ + kKTileBytes - 1) / kKTileBytes);
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+  // ---- main loop: PF k-tiles in registers, 2-stage LDS ring --------------
+  // k-tile j lives in R[j % PF] and is loaded PF-1 iterations before the
+  // iteration that moves it to LDS.  Loads past the last k-tile read zeros
+  // (buffer range check), so the steady-state loop issues every load and
+  // store unconditionally and the compiler's count of outstanding loads stays
+  // exact; the last nk % PF k-tiles run in a guarded tail.
+  if (nk > 0) {
+    StageRegs<IN_DT> R[PF];
+#pragma unroll
+    for (int q = 0; q < PF; ++q) R[q].load(tl, q, t);
+    R[0].store(smem, t);
+    R[0].load(tl, PF, t);
+    __syncthreads();
+    const int nfull = nk - nk % PF;
+    for (int t0 = 0; t0 < nfull; t0 += PF) {
+#pragma unroll
+      for (int q = 0; q < PF; ++q) {
+        const int kt = t0 + q;
+        mma_stage<IN_DT>(smem + (kt & 1) * STAGE_BYTES, lane, wm, wn, acc);
+        R[(q + 1) % PF].store(smem + ((kt + 1) & 1) * STAGE_BYTES, t);
+        R[(q + 1) % PF].load(tl, kt + 1 + PF, t);
+        __syncthreads();
+      }
+    }
+#pragma unroll
+    for (int q = 0; q + 1 < PF; ++q) {
+      const int kt = nfull + q;
+      if (kt < nk) {
+        mma_stage<IN_DT>(smem + (kt & 1) * STAGE_BYTES, lane, wm, wn, acc);
+        R[(q + 1) % PF].store(smem + ((kt + 1) & 1) * STAGE_BYTES, t);
+        __syncthreads();
+      }
+    }
+  }
+
+  // ---- epilogue --------------------------------------------------------------
+  // Lane owns output rows m_loc(mt) = wm*64 + mt*32 + lane%32 and, for each
+  // nt, the 16 columns n_loc = wn*64 + nt*32 + acc_i(lane, v).
+  const int jr = acc_j(lane);
+  if constexpr (EPI == kEpiLogits) {
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int nt2 = 0; nt2 < 2; ++nt2)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[mt][nt2][v] *= p.lin_scale;
+  } else {
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int nt2 = 0; nt2 < 2; ++nt2)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int64_t n = n0 + wn * 64 + nt2 * 32 + acc_i(lane, v);
+          float y = acc[mt][nt2][v] * p.c2;
+          y = (n < p.N) ? y : -INFINITY;
+          acc[mt][nt2][v] = y;
+          mx = fmaxf(mx, y);
+        }
+      mx = wave_xor32_max(mx);
+      if (lane < 32) redmax[wn * BM + wm * 64 + mt * 32 + jr] = mx;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      const int row = wm * 64 + mt * 32 + jr;
+      const float tmax = fmaxf(redmax[row], redmax[BM + row]);
+      float sm = 0.0f;
+#pragma unroll
+      for (int nt2 = 0; nt2 < 2; ++nt2)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const float e = __builtin_amdgcn_exp2f(acc[mt][nt2][v] - tmax);
+          acc[mt][nt2][v] = e;
+          sm += e;
+        }
+      sm = wave_xor32_sum(sm);
+      if (lane < 32) redsum[wn * BM + row] = sm;
+    }
+    __syncthreads();
+
+    // Publish this tile's row statistics.
+    if (t < BM) {
+      const float tm = fmaxf(redmax[t], redmax[BM + t]);
+      const float ts = redsum[t] + redsum[BM + t];
+      store_stat(p.partial + (rbg * BM + t) * p.nT + nt, tm, ts);
+      factor[t] = 1.0f;
+    }
+    if constexpr (EPI == kEpiExchange) {
+      if (t < BM) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+      __syncthreads();
+      if (t == 0) rowblock_barrier(p.sync + 2 * rbg, p.nT, p.err, p.spin_ticks);
+      __syncthreads();
+      if (t < BM) {
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        const float2* st = p.partial + (rbg * BM + t) * p.nT;
+        float gm = -INFINITY, gs = 0.0f;
+        for (int q = 0; q < p.nT; ++q) {  // online merge of (max, sum) pairs
+          const float2 s = load_stat(st + q);
+          const float nm = fmaxf(gm, s.x);
+          gs = gs * __builtin_amdgcn_exp2f(gm - nm) + s.y * __builtin_amdgcn_exp2f(s.x - nm);
+          gm = nm;
+        }
+        const float tm = fmaxf(redmax[t], redmax[BM + t]);
+        factor[t] = __builtin_amdgcn_exp2f(tm - gm) / gs;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      const float f = factor[wm * 64 + mt * 32 + jr];
+#pragma unroll
+      for (int nt2 = 0; nt2 < 2; ++nt2)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[mt][nt2][v] *= f;
+    }
+  }
+
+  // ---- stage the tile in LDS, then 128-bit coalesced stores ------------------
+  constexpr int OSZ = OutTraits<OUT_DT>::SZ;
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+    for (int nt2 = 0; nt2 < 2; ++nt2)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int m_loc = wm * 64 + mt * 32 + jr;
+        const int n_loc = wn * 64 + nt2 * 32 + acc_i(lane, 4 * g);
+        store4<OUT_DT>(smem + m_loc * L::PITCH + n_loc * OSZ, acc[mt][nt2][4 * g],
+                       acc[mt][nt2][4 * g + 1], acc[mt][nt2][4 * g + 2], acc[mt][nt2][4 * g + 3]);
+      }
+  __syncthreads();
+  constexpr int CPR = BN * OSZ / 16;  // 16-byte chunks per tile row
+  constexpr int EPC = 16 / OSZ;       // elements per chunk
+#pragma unroll 4
+  for (int idx = t; idx < BM * CPR; idx += NTHREADS) {
+    const int row = idx / CPR, ch = idx % CPR;
+    const int64_t m = row0 + row;
+    const int64_t n = n0 + ch * EPC;
+    if (m < p.M && n < p.N) {
+      const u32x4 u = *reinterpret_cast<const u32x4*>(smem + row * L::PITCH + ch * 16);
+      *reinterpret_cast<u32x4*>(o_base + m * p.ldo_bytes + n * OSZ) = u;
+    }
+  }
+}
+
+// -------------------------------------------------------------------------
+// Second pass of the split (online two-pass) softmax: one wave per row.
+// Merges the row's nT tile statistics into (max, sum), then rescales the
+// tile-relative exponentials in place: out *= exp2(m_t - M) / S.
+// -------------------------------------------------------------------------
+template <int OUT_DT>
+__global__ void __launch_bounds__(256)
+rescale_rows_kernel(uint8_t* __restrict__ out, const float2* __restrict__ partial,
+                    int64_t rows_total, int64_t M, int64_t nRB, int64_t N,
+                    int64_t ldo_bytes, int64_t o_bstride, int nT) {
+  constexpr int ROWS_PER_WG = 4;
+  constexpr int MAX_NT = 512;
+  __shared__ float fac[ROWS_PER_WG][MAX_NT];
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t grow = (int64_t)blockIdx.x * ROWS_PER_WG + w;  // row over batch*M
+  const bool live = grow < rows_total;
+  int64_t bt = 0, m = 0;
+  if (live) {
+    bt = grow / M;
+    m = grow % M;
+    const int64_t rbg = bt * nRB + m / BM;
+    const float2* st = partial + (rbg * BM + (m % BM)) * nT;
+    float gm = -INFINITY;
+    for (int q = lane; q < nT; q += 64) gm = fmaxf(gm, st[q].x);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) gm = fmaxf(gm, __shfl_xor(gm, off));
+    float gs = 0.0f;
+    for (int q = lane; q < nT; q += 64) gs += st[q].y * __builtin_amdgcn_exp2f(st[q].x - gm);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) gs += __shfl_xor(gs, off);
+    const float inv = 1.0f / gs;
+    for (int q = lane; q < nT; q += 64) fac[w][q] = __builtin_amdgcn_exp2f(st[q].x - gm) * inv;
+  }
+  __syncthreads();
+  if (!live) return;
+  constexpr int OSZ = OutTraits<OUT_DT>::SZ;
+  constexpr int EPC = 16 / OSZ;
+  uint8_t* rowp = out + bt * o_bstride + m * ldo_bytes;
+  for (int64_t c = lane; c * EPC < N; c += 64) {
+    const int64_t n = c * EPC;
+    const float f = fac[w][n / BN];
+    u32x4 u = *reinterpret_cast<const u32x4*>(rowp + n * OSZ);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t x = u[e];
+      uint32_t y;
+      if constexpr (OUT_DT == DT_F32) {
+        y = __builtin_bit_cast(uint32_t, __builtin_bit_cast(float, x) * f);
+      } else if constexpr (OUT_DT == DT_F16) {
+        const uint16_t lo = (uint16_t)(x & 0xFFFFu), hi = (uint16_t)(x >> 16);
+        const float x0 = (float)__builtin_bit_cast(_Float16, lo) * f;
+        const float x1 = (float)__builtin_bit_cast(_Float16, hi) * f;
+        y = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x0) |
+            ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x1) << 16);
+      } else {
+        const uint32_t lo = x << 16, hi = x & 0xFFFF0000u;
+        const float x0 = __builtin_bit_cast(float, lo) * f;
+        const float x1 = __builtin_bit_cast(float, hi) * f;
+        y = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x0) |
+            ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x1) << 16);
+      }
+      u[e] = y;
+    }
+    *reinterpret_cast<u32x4*>(rowp + n * OSZ) = u;
+  }
+}
+
+// Zero fill with a kernel (no hipMemset, so it may sit inside a captured graph).
+__global__ void zero_words_kernel(uint32_t* __restrict__ p, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = 0u;
+}
+
+// -------------------------------------------------------------------------
+// Instantiation table
+// -------------------------------------------------------------------------
+constexpr int kPF = 3;
+
+template <int IN_DT, int OUT_DT, int EPI>
+static const void* tile_kernel_ptr() {
+  return reinterpret_cast<const void*>(&chain_tile_kernel<IN_DT, OUT_DT, EPI, kPF>);
+}
+
+template <int IN_DT, int EPI>
+static const void* by_out(int out_dt) {
+  switch (out_dt) {
+    case DT_F32: return tile_kernel_ptr<IN_DT, DT_F32, EPI>();
+    case DT_F16: return tile_kernel_ptr<IN_DT, DT_F16, EPI>();
+    case DT_BF16: return tile_kernel_ptr<IN_DT, DT_BF16, EPI>();
+  }
+  return nullptr;
+}
+
+template <int EPI>
+static const void* by_in(int in_dt, int out_dt) {
+  switch (in_dt) {
+    case DT_F32: return by_out<DT_F32, EPI>(out_dt);
+    case DT_F16: return by_out<DT_F16, EPI>(out_dt);
+    case DT_BF16: return by_out<DT_BF16, EPI>(out_dt);
+    case DT_FP8: return by_out<DT_FP8, EPI>(out_dt);
+  }
+  return nullptr;
+}
+
+const void* chain_kernel_symbol(int in_dt, int out_dt, int epi) {
+  if (epi == kEpiExchange) return by_in<kEpiExchange>(in_dt, out_dt);
+  if (epi == kEpiSplit) return by_in<kEpiSplit>(in_dt, out_dt);
+  if (epi == kEpiLogits) return by_in<kEpiLogits>(in_dt, out_dt);
+  return nullptr;
+}
+
+const void* rescale_kernel_symbol(int out_dt) {
+  switch (out_dt) {
+    case DT_F32: return reinterpret_cast<const void*>(&rescale_rows_kernel<DT_F32>);
+    case DT_F16: return reinterpret_cast<const void*>(&rescale_rows_kernel<DT_F16>);
+    case DT_BF16: return reinterpret_cast<const void*>(&rescale_rows_kernel<DT_BF16>);
+  }
+  return nullptr;
+}
+
+const void* zero_kernel_symbol() { return reinterpret_cast<const void*>(&zero_words_kernel); }
+
+int chain_kernel_lds_bytes(int out_dt) {
+  switch (out_dt) {
+    case DT_F32: return EpiLayout<DT_F32>::TOTAL;
+    case DT_F16: return EpiLayout<DT_F16>::TOTAL;
+    case DT_BF16: return EpiLayout<DT_BF16>::TOTAL;
+  }
+  return 0;
+}
+
+}  // namespace wtc

@@ -1,0 +1,363 @@
+// launch.hip -- host side of the launcher C-ABI (include/wtc/wtc_hip.h):
+// argument checks, the launch plan, the per-device default workspace, and
+// the kernel launches for the exchange, split and unfused paths.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+
+#include "tile_layout.h"
+#include "wtc/wtc_hip.h"
+#include "wtc_kernels.h"
+
+namespace {
+
+using namespace wtc;
+
+constexpr int kTile = 128;            // BM = BN of chain_tile_kernel
+constexpr int kThreads = 256;
+constexpr int kRescaleRowsPerWg = 4;  // rescale_rows_kernel
+constexpr int kRescaleMaxTiles = 512;
+constexpr uint64_t kSpinTicks = 200000000ull;  // 2 s of the 100 MHz clock
+constexpr int kMaxDevices = 64;
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string& msg) {
+  g_last_error = msg;
+  return code;
+}
+
+int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
+
+bool valid_in(int dt) { return dt == DT_F32 || dt == DT_F16 || dt == DT_BF16 || dt == DT_FP8; }
+bool valid_out(int dt) { return dt == DT_F32 || dt == DT_F16 || dt == DT_BF16; }
+
+// Workspace layout (bytes):
+//   [0, 256)              error flags (u32 at 0)
+//   [256, +sync)          row-block counter/generation pairs
+//   [.., +partial)        per-tile row statistics, float2 [rows_pad][nT]
+//   [.., +logits)         unfused path only: f32 logits, row max, row sum
+struct WsLayout {
+  int64_t sync_off, sync_bytes;
+  int64_t partial_off, partial_bytes;
+  int64_t logits_off, max_off, sum_off;
+  int64_t total;
+};
+
+WsLayout ws_layout(int64_t batch, int64_t m, int64_t n, int path) {
+  WsLayout w{};
+  const int64_t nRB = ceil_div(m, kTile), nT = ceil_div(n, kTile);
+  const int64_t rbs = batch * nRB;
+  w.sync_off = 256;
+  w.sync_bytes = align256(rbs * 2 * 4);
+  w.partial_off = w.sync_off + w.sync_bytes;
+  w.partial_bytes = align256(rbs * kTile * nT * 8);
+  w.total = w.partial_off + w.partial_bytes;
+  if (path == WTC_PATH_UNFUSED) {
+    w.logits_off = w.total;
+    w.max_off = w.logits_off + align256(batch * m * n * 4);
+    w.sum_off = w.max_off + align256(batch * m * 4);
+    w.total = w.sum_off + align256(batch * m * 4);
+  }
+  return w;
+}
+
+int check_args(int64_t batch, int64_t m, int64_t n, int64_t k, int in_dt, int out_dt,
+               int path) {
+  if (batch < 0 || m < 0 || n < 0 || k < 0)
+    return fail(WTC_ERR_ARG, "negative extent");
+  if (!valid_in(in_dt)) return fail(WTC_ERR_ARG, "unsupported in_dtype");
+  if (!valid_out(out_dt)) return fail(WTC_ERR_ARG, "unsupported out_dtype");
+  if (path < WTC_PATH_AUTO || path > WTC_PATH_UNFUSED)
+    return fail(WTC_ERR_ARG, "unknown path");
+  if ((k * dtype_bytes(in_dt)) % 16 != 0)
+    return fail(WTC_ERR_ARG, "k * element bytes must be a multiple of 16");
+  if (n % 8 != 0) return fail(WTC_ERR_ARG, "n must be a multiple of 8");
+  // Buffer descriptors address one batch slice of A, B, out with 32-bit offsets.
+  const int64_t isz = dtype_bytes(in_dt), osz = dtype_bytes(out_dt);
+  const int64_t lim = 0x7FFFFFFFll;
+  if (m * k * isz > lim || k * n * isz > lim || m * n * osz > lim || m * n * 4 > lim)
+    return fail(WTC_ERR_UNSUPPORTED, "one batch slice of A, B or out exceeds 2 GiB");
+  return WTC_OK;
+}
+
+int plan_impl(int64_t batch, int64_t m, int64_t n, int64_t k, int in_dt, int out_dt,
+              int path, int cu_count, int wg_per_cu, int64_t* grid, int* chosen,
+              int64_t* ws_bytes) {
+  int rc = check_args(batch, m, n, k, in_dt, out_dt, path);
+  if (rc) return rc;
+  const int64_t tiles = batch * ceil_div(m, kTile) * ceil_div(n, kTile);
+  const int64_t capacity = (int64_t)cu_count * (int64_t)wg_per_cu;
+  int p = path;
+  if (p == WTC_PATH_AUTO) p = (tiles <= capacity) ? WTC_PATH_EXCHANGE : WTC_PATH_SPLIT;
+  if (p == WTC_PATH_EXCHANGE && tiles > capacity)
+    return fail(WTC_ERR_UNSUPPORTED,
+                "exchange path needs every tile co-resident: " + std::to_string(tiles) +
+                    " tiles > " + std::to_string(capacity) + " resident workgroups");
+  if (p == WTC_PATH_SPLIT && ceil_div(n, kTile) > kRescaleMaxTiles)
+    return fail(WTC_ERR_UNSUPPORTED, "split path supports n <= 65536");
+  if (tiles > 0x7FFFFFFFll) return fail(WTC_ERR_UNSUPPORTED, "too many tiles for one grid");
+  if (grid) *grid = tiles;
+  if (chosen) *chosen = p;
+  if (ws_bytes) *ws_bytes = ws_layout(batch, m, n, p).total;
+  return WTC_OK;
+}
+
+struct DeviceState {
+  bool init = false;
+  int cu_count = 0;
+  int occ[4][3] = {};  // exchange-kernel workgroups per CU, [in_dt][out_dt]
+  void* ws = nullptr;
+  size_t ws_bytes = 0;
+};
+
+std::mutex g_mu;
+DeviceState g_dev[kMaxDevices];
+
+#define HIP_TRY(expr)                                                              \
+  do {                                                                             \
+    hipError_t e_ = (expr);                                                        \
+    if (e_ != hipSuccess)                                                          \
+      return fail(WTC_ERR_HIP, std::string(#expr) + ": " + hipGetErrorString(e_)); \
+  } while (0)
+
+// Dynamic LDS added to the exchange kernel so that no CU holds two of its
+// workgroups (spreads a grid of <= CU-count tiles over all CUs).
+int exchange_lds_pad(int out_dt) {
+  const int stat = chain_kernel_lds_bytes(out_dt);
+  const int want = 80 * 1024 + 1024;
+  return stat >= want ? 0 : want - stat;
+}
+
+int device_state(int dev, DeviceState** out) {
+  if (dev < 0 || dev >= kMaxDevices) return fail(WTC_ERR_HIP, "device index out of range");
+  DeviceState& s = g_dev[dev];
+  if (!s.init) {
+    hipDeviceProp_t prop;
+    HIP_TRY(hipGetDeviceProperties(&prop, dev));
+    s.cu_count = prop.multiProcessorCount;
+    for (int i = 0; i < 4; ++i)
+      for (int o = 0; o < 3; ++o) {
+        const void* fn = chain_kernel_symbol(i, o, kEpiExchange);
+        const int pad = exchange_lds_pad(o);
+        HIP_TRY(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, pad));
+        int nb = 0;
+        HIP_TRY(hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, fn, kThreads, pad));
+        s.occ[i][o] = nb;
+      }
+    s.init = true;
+  }
+  *out = &s;
+  return WTC_OK;
+}
+
+int zero_fill(void* p, int64_t bytes, hipStream_t stream) {
+  const int64_t words = bytes / 4;
+  if (words <= 0) return WTC_OK;
+  int64_t blocks = ceil_div(words, 256);
+  if (blocks > 4096) blocks = 4096;
+  uint32_t* ptr = static_cast<uint32_t*>(p);
+  int64_t n = words;
+  void* args[] = {&ptr, &n};
+  HIP_TRY(hipLaunchKernel(zero_kernel_symbol(), dim3((unsigned)blocks), dim3(256), args, 0, stream));
+  return WTC_OK;
+}
+
+int default_workspace(DeviceState* s, int64_t need, void** ws, hipStream_t stream) {
+  if ((int64_t)s->ws_bytes < need) {
+    if (s->ws) HIP_TRY(hipFree(s->ws));
+    s->ws = nullptr;
+    s->ws_bytes = 0;
+    const int64_t bytes = need < (1 << 20) ? (1 << 20) : need;
+    HIP_TRY(hipMalloc(&s->ws, (size_t)bytes));
+    s->ws_bytes = (size_t)bytes;
+    int rc = zero_fill(s->ws, bytes, stream);
+    if (rc) return rc;
+  }
+  *ws = s->ws;
+  return WTC_OK;
+}
+
+int launch_chain(const void* kern, int64_t grid, int lds_dyn, const ChainParams& prm,
+                 hipStream_t stream) {
+  ChainParams p = prm;
+  void* args[] = {&p};
+  HIP_TRY(hipLaunchKernel(kern, dim3((unsigned)grid), dim3(kThreads), args, (size_t)lds_dyn, stream));
+  return WTC_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* wtc_last_error(void) { return g_last_error.c_str(); }
+
+const char* wtc_version(void) { return "wtc-mi355x 0.1.0 (gfx950)"; }
+
+int wtc_plan(int64_t batch, int64_t m, int64_t n, int64_t k, int in_dtype, int out_dtype,
+             int path, int cu_count, int wg_per_cu, int64_t* grid, int* chosen_path,
+             int64_t* workspace_bytes) {
+  g_last_error.clear();
+  return plan_impl(batch, m, n, k, in_dtype, out_dtype, path, cu_count, wg_per_cu, grid,
+                   chosen_path, workspace_bytes);
+}
+
+int64_t wtc_matmul_softmax_workspace_size(int64_t batch, int64_t m, int64_t n, int64_t k,
+                                          int in_dtype, int out_dtype, int path) {
+  g_last_error.clear();
+  if (check_args(batch, m, n, k, in_dtype, out_dtype, path)) return -1;
+  return ws_layout(batch, m, n, path).total;
+}
+
+int wtc_workspace_init(void* workspace, size_t workspace_bytes, void* stream) {
+  g_last_error.clear();
+  if (!workspace && workspace_bytes) return fail(WTC_ERR_ARG, "workspace is NULL");
+  return zero_fill(workspace, (int64_t)workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+int wtc_read_error_flags(void* workspace, uint32_t* flags, int clear) {
+  g_last_error.clear();
+  if (!flags) return fail(WTC_ERR_ARG, "flags is NULL");
+  void* ws = workspace;
+  if (!ws) {
+    int dev = 0;
+    HIP_TRY(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (dev < 0 || dev >= kMaxDevices || !g_dev[dev].ws) {
+      *flags = 0;
+      return WTC_OK;
+    }
+    ws = g_dev[dev].ws;
+  }
+  HIP_TRY(hipDeviceSynchronize());
+  HIP_TRY(hipMemcpy(flags, ws, 4, hipMemcpyDeviceToHost));
+  if (clear) {
+    uint32_t zero = 0;
+    HIP_TRY(hipMemcpy(ws, &zero, 4, hipMemcpyHostToDevice));
+  }
+  return WTC_OK;
+}
+
+int wtc_matmul_softmax(const void* a, const void* b, void* out, int64_t batch, int64_t m,
+                       int64_t n, int64_t k, int in_dtype, int out_dtype, float logit_scale,
+                       float scale_a, float scale_b, int path, void* workspace,
+                       size_t workspace_bytes, void* stream_) {
+  g_last_error.clear();
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  int rc = check_args(batch, m, n, k, in_dtype, out_dtype, path);
+  if (rc) return rc;
+  if (batch == 0 || m == 0 || n == 0) return WTC_OK;
+  if (!out || (k > 0 && (!a || !b))) return fail(WTC_ERR_ARG, "null data pointer");
+  if ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b) |
+       reinterpret_cast<uintptr_t>(out)) & 15u)
+    return fail(WTC_ERR_ARG, "data pointers must be 16-byte aligned");
+  if (!std::isfinite(logit_scale) || !std::isfinite(scale_a) || !std::isfinite(scale_b))
+    return fail(WTC_ERR_ARG, "scales must be finite");
+
+  int dev = 0;
+  HIP_TRY(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lk(g_mu);
+  DeviceState* ds = nullptr;
+  rc = device_state(dev, &ds);
+  if (rc) return rc;
+
+  int64_t grid = 0, need = 0;
+  int chosen = 0;
+  rc = plan_impl(batch, m, n, k, in_dtype, out_dtype, path, ds->cu_count,
+                 ds->occ[in_dtype][out_dtype], &grid, &chosen, &need);
+  if (rc) return rc;
+
+  void* ws = workspace;
+  if (ws) {
+    if ((int64_t)workspace_bytes < need)
+      return fail(WTC_ERR_WORKSPACE, "workspace needs " + std::to_string(need) + " bytes");
+    if (reinterpret_cast<uintptr_t>(ws) & 255u)
+      return fail(WTC_ERR_ARG, "workspace must be 256-byte aligned");
+  } else {
+    rc = default_workspace(ds, need, &ws, stream);
+    if (rc) return rc;
+  }
+  const WsLayout L = ws_layout(batch, m, n, chosen);
+  uint8_t* wsb = static_cast<uint8_t*>(ws);
+
+  const int isz = dtype_bytes(in_dtype), osz = dtype_bytes(out_dtype);
+  const float lin = logit_scale * scale_a * scale_b;
+  ChainParams p{};
+  p.a = static_cast<const uint8_t*>(a);
+  p.b = static_cast<const uint8_t*>(b);
+  p.out = static_cast<uint8_t*>(out);
+  p.M = m;
+  p.N = n;
+  p.K = k;
+  p.a_bstride = m * k * isz;
+  p.b_bstride = k * n * isz;
+  p.o_bstride = m * n * osz;
+  p.lda_bytes = k * isz;
+  p.ldb_bytes = n * isz;
+  p.ldo_bytes = n * osz;
+  p.c2 = lin * 1.4426950408889634f;
+  p.lin_scale = lin;
+  p.nRB = (int)ceil_div(m, kTile);
+  p.nT = (int)ceil_div(n, kTile);
+  p.partial = reinterpret_cast<float2*>(wsb + L.partial_off);
+  p.sync = reinterpret_cast<uint32_t*>(wsb + L.sync_off);
+  p.err = reinterpret_cast<uint32_t*>(wsb);
+  p.spin_ticks = kSpinTicks;
+
+  if (chosen == WTC_PATH_EXCHANGE) {
+    return launch_chain(chain_kernel_symbol(in_dtype, out_dtype, kEpiExchange), grid,
+                        exchange_lds_pad(out_dtype), p, stream);
+  }
+  if (chosen == WTC_PATH_SPLIT) {
+    rc = launch_chain(chain_kernel_symbol(in_dtype, out_dtype, kEpiSplit), grid, 0, p, stream);
+    if (rc) return rc;
+    uint8_t* o = p.out;
+    const float2* part = p.partial;
+    int64_t rows_total = batch * m, M_ = m, nRB = p.nRB, N_ = n, ldo = p.ldo_bytes,
+            ob = p.o_bstride;
+    int nT = p.nT;
+    void* args[] = {&o, &part, &rows_total, &M_, &nRB, &N_, &ldo, &ob, &nT};
+    HIP_TRY(hipLaunchKernel(rescale_kernel_symbol(out_dtype),
+                            dim3((unsigned)ceil_div(rows_total, kRescaleRowsPerWg)), dim3(256),
+                            args, 0, stream));
+    return WTC_OK;
+  }
+  // Unfused: logits (f32) into the workspace, then four row kernels.
+  float* logits = reinterpret_cast<float*>(wsb + L.logits_off);
+  float* rmax = reinterpret_cast<float*>(wsb + L.max_off);
+  float* rsum = reinterpret_cast<float*>(wsb + L.sum_off);
+  ChainParams q = p;
+  q.out = reinterpret_cast<uint8_t*>(logits);
+  q.o_bstride = m * n * 4;
+  q.ldo_bytes = n * 4;
+  rc = launch_chain(chain_kernel_symbol(in_dtype, DT_F32, kEpiLogits), grid, 0, q, stream);
+  if (rc) return rc;
+  const int64_t rows = batch * m;
+  if (rows > 0x7FFFFFFFll) return fail(WTC_ERR_UNSUPPORTED, "too many rows");
+  int64_t N_ = n;
+  {
+    void* args[] = {&logits, &rmax, &N_};
+    HIP_TRY(hipLaunchKernel(rowmax_kernel_symbol(), dim3((unsigned)rows), dim3(256), args, 0, stream));
+  }
+  {
+    void* args[] = {&logits, &rmax, &N_};
+    HIP_TRY(hipLaunchKernel(expsub_kernel_symbol(), dim3((unsigned)rows), dim3(256), args, 0, stream));
+  }
+  {
+    void* args[] = {&logits, &rsum, &N_};
+    HIP_TRY(hipLaunchKernel(rowsum_kernel_symbol(), dim3((unsigned)rows), dim3(256), args, 0, stream));
+  }
+  {
+    void* o = out;
+    void* args[] = {&logits, &rsum, &o, &N_};
+    HIP_TRY(hipLaunchKernel(rowdiv_kernel_symbol(out_dtype), dim3((unsigned)rows), dim3(256), args, 0, stream));
+  }
+  return WTC_OK;
+}
+
+}  // extern "C"

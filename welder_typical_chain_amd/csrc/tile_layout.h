@@ -1,0 +1,119 @@
+// tile_layout.h -- index maps of the fused Matmul->row-Softmax kernels for
+// gfx950.  Everything here is plain integer arithmetic usable on host and
+// device, so the CPU test (tests/layout_check.cpp) can replay one workgroup's
+// data movement and check it against a plain matmul.
+//
+// Vocabulary.
+//   chunk   16 contiguous bytes along K (8 f16/bf16, 16 fp8, 4 f32).  One
+//           chunk is what a lane hands one MFMA-operand register quad.
+//   k-tile  128 bytes of K (8 chunks) staged per pipeline step.
+//   tile    BM x BN block of the output owned by one workgroup.
+//   row block  BM rows of one batch: the tiles that share a softmax row.
+//
+// LDS layout of one pipeline stage (both operands k-contiguous so every
+// MFMA operand fetch is a single ds_read_b128):
+//   A: [BM rows][8 chunks], chunk c of row m stored at slot c ^ ((m>>1)&7).
+//      16 lanes reading 16 consecutive rows at one chunk hit 16 distinct
+//      4-bank groups; the 16 lanes of a store (2 rows x 8 chunks) do too.
+//   B: [8 chunks][BN cols], column n of chunk row kc stored at
+//      n ^ ((n>>4)&3).  The B tile arrives N-contiguous from HBM and is
+//      transposed in registers before this store (B is [K,N] row-major).
+#pragma once
+#include <stdint.h>
+
+#if defined(__HIPCC__)
+#define WTC_HD __host__ __device__ inline
+#else
+#define WTC_HD inline
+#endif
+
+namespace wtc {
+
+enum : int { DT_F32 = 0, DT_F16 = 1, DT_BF16 = 2, DT_FP8 = 3 };
+
+WTC_HD constexpr int dtype_bytes(int dt) {
+  return dt == DT_F32 ? 4 : (dt == DT_FP8 ? 1 : 2);
+}
+
+constexpr int kChunkBytes = 16;
+constexpr int kKTileBytes = 128;
+constexpr int kChunksPerKTile = kKTileBytes / kChunkBytes; // 8
+
+// ---- A operand (row-major [M,K]) ----------------------------------------
+// Byte offset of (row m, chunk c) inside the A stage buffer.
+WTC_HD constexpr int a_lds_offset(int m, int c) {
+  return m * kKTileBytes + ((c ^ ((m >> 1) & 7)) * kChunkBytes);
+}
+// Every thread fetches part of both operands (straight-line code, so the
+// compiler can count outstanding loads exactly).  A: thread t, pass j (0..3)
+// fetches chunk t%8 of row t/8 + 32j with one 128-bit load; the 8 lanes of a
+// row cover its 128 contiguous bytes.
+WTC_HD constexpr int a_load_row(int t, int j) { return (t >> 3) + 32 * j; }
+WTC_HD constexpr int a_load_chunk(int t) { return t & 7; }
+
+// ---- B operand (row-major [K,N]) ----------------------------------------
+// Column n of chunk row kc is stored at slot n ^ ((n>>4)&7): 16 consecutive
+// columns (a fragment read) and the 16 columns 4g+c, g = 0..15 (one store
+// instruction of 16 loader lanes) both land in 16 distinct slots mod 16.
+WTC_HD constexpr int b_swz(int n) { return n ^ ((n >> 4) & 7); }
+// Byte offset of (chunk row kc, column n) inside the B stage buffer of width BN.
+WTC_HD constexpr int b_lds_offset(int kc, int n, int BN) {
+  return (kc * BN + b_swz(n)) * kChunkBytes;
+}
+// B: thread t owns columns 4*(t%32)+0..3 of the k-rows of chunk row
+// kc = t/32: an (elements-per-chunk) x 4 block that it transposes into 4
+// chunks, one per column.  32 lanes cover 128 contiguous columns.
+WTC_HD constexpr int b_load_colgroup(int t) { return t & 31; }
+WTC_HD constexpr int b_load_chunkrow(int t) { return t >> 5; }
+
+// ---- MFMA fragments (32x32xK, wave64) -------------------------------------
+// Lane l supplies row/col (l % 32) and chunk (2*s + l/32) of k-substep s.
+WTC_HD constexpr int frag_row(int lane) { return lane & 31; }
+WTC_HD constexpr int frag_chunk(int lane, int s) { return 2 * s + (lane >> 5); }
+// 32x32 accumulator: register v of lane l holds D[i][j] with
+// j = l % 32 and i = 8*(v/4) + 4*(l/32) + v%4.
+WTC_HD constexpr int acc_i(int lane, int v) {
+  return 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+}
+WTC_HD constexpr int acc_j(int lane) { return lane & 31; }
+
+// ---- register transpose of B (N-contiguous rows -> K-contiguous chunks) ---
+// 16-bit elements: `lo`/`hi` hold columns (2*(c/2), 2*(c/2)+1) of k-rows 2w
+// and 2w+1; returns word w of the chunk of column c (two consecutive k).
+WTC_HD constexpr uint32_t transpose16_word(uint32_t lo, uint32_t hi, int c) {
+  return (c & 1) ? ((lo >> 16) | (hi & 0xFFFF0000u)) : ((lo & 0xFFFFu) | (hi << 16));
+}
+// 8-bit elements: r0..r3 hold columns 0..3 of k-rows 4w..4w+3; returns word w
+// of the chunk of column c (four consecutive k).
+WTC_HD constexpr uint32_t transpose8_word(uint32_t r0, uint32_t r1, uint32_t r2,
+                                          uint32_t r3, int c) {
+  return ((r0 >> (8 * c)) & 0xFFu) | (((r1 >> (8 * c)) & 0xFFu) << 8) |
+         (((r2 >> (8 * c)) & 0xFFu) << 16) | (((r3 >> (8 * c)) & 0xFFu) << 24);
+}
+
+// A B loader holds its k-rows as 16 row-major 32-bit words (4 columns per
+// row: 2 words of f16/bf16, 1 of fp8, 4 of f32).  Index of the word holding
+// column c of k-row r:
+WTC_HD constexpr int b_src_word(int sz, int r, int c) {
+  return sz == 2 ? r * 2 + (c >> 1) : (sz == 1 ? r : r * 4 + c);
+}
+// Word w of the K-contiguous chunk of column c, from the loader's words.
+template <typename Words>
+WTC_HD uint32_t b_unit_word(const Words& rw, int sz, int c, int w) {
+  if (sz == 2) return transpose16_word(rw(b_src_word(2, 2 * w, c)), rw(b_src_word(2, 2 * w + 1, c)), c);
+  if (sz == 1)
+    return transpose8_word(rw(b_src_word(1, 4 * w, c)), rw(b_src_word(1, 4 * w + 1, c)),
+                           rw(b_src_word(1, 4 * w + 2, c)), rw(b_src_word(1, 4 * w + 3, c)), c);
+  return rw(b_src_word(4, w, c));
+}
+
+// ---- workgroup -> tile ------------------------------------------------------
+// Workgroups are dispatched round-robin over the 8 XCDs (blockIdx % 8).
+// Remap so that XCD x receives the contiguous tile range
+// [x*G/8, (x+1)*G/8): the tiles of a row block (consecutive ids) then share
+// one XCD's L2 and their row-statistics exchange stays on that XCD.
+WTC_HD constexpr int64_t xcd_remap(int64_t b, int64_t G) {
+  return (G % 8 == 0) ? (b % 8) * (G / 8) + b / 8 : b;
+}
+
+} // namespace wtc

@@ -1,0 +1,41 @@
+// wtc_kernels.h -- kernel parameter block and symbol table shared by the
+// HIP kernels (fused_matmul_softmax.hip, unfused_chain.hip) and the host
+// launcher (launch.hip).  Internal to the library; the public C-ABI is
+// include/wtc/wtc_hip.h.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace wtc {
+
+enum : int { kEpiExchange = 0, kEpiSplit = 1, kEpiLogits = 2 };
+
+struct ChainParams {
+  const uint8_t* a;
+  const uint8_t* b;
+  uint8_t* out;
+  int64_t M, N, K;                       // per batch
+  int64_t a_bstride, b_bstride, o_bstride;  // bytes between batches
+  int64_t lda_bytes, ldb_bytes, ldo_bytes;  // row pitches in bytes
+  float c2;         // scale * log2(e): softmax runs as exp2(c2*x - max)
+  float lin_scale;  // scale for kEpiLogits
+  int nRB;          // row blocks (of 128 rows) per batch
+  int nT;           // column tiles (of 128 columns) per row block
+  float2* partial;  // [batch*nRB*128][nT] per-tile row (max, sumexp), log2 domain
+  uint32_t* sync;   // [batch*nRB][2] row-block counter and generation
+  uint32_t* err;    // bit 0: a row-block wait timed out
+  uint64_t spin_ticks;  // row-block wait limit, 100 MHz ticks
+};
+
+const void* chain_kernel_symbol(int in_dt, int out_dt, int epi);
+const void* rescale_kernel_symbol(int out_dt);
+const void* zero_kernel_symbol();
+int chain_kernel_lds_bytes(int out_dt);
+
+// Unfused five-kernel baseline (matmul, row max, exp, row sum, divide).
+const void* rowmax_kernel_symbol();
+const void* expsub_kernel_symbol();
+const void* rowsum_kernel_symbol();
+const void* rowdiv_kernel_symbol(int out_dt);
+
+}  // namespace wtc
