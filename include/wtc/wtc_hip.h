@@ -78,9 +78,11 @@ int wtc_plan(int64_t batch, int64_t m, int64_t n, int64_t k, int in_dtype,
              int out_dtype, int path, int cu_count, int wg_per_cu,
              int64_t *grid, int *chosen_path, int64_t *workspace_bytes);
 
-/* Reads (and with clear != 0, resets) the device error flags of a workspace
- * (NULL = the default workspace of the current device).  Bit 0: a row-block
- * wait of the exchange path timed out.  Synchronises the device. */
+/* Reads (and with clear != 0, resets) the three diagnostic words of a
+ * workspace (NULL = the default workspace of the current device) into
+ * flags[0..2]: flags[0] bit 0 = a row-block wait of the exchange path timed
+ * out, flags[1] = longest row-block wait in 100 MHz ticks, flags[2] = number
+ * of timed-out waits.  Synchronises the device. */
 int wtc_read_error_flags(void *workspace, uint32_t *flags, int clear);
 
 /* Message of the last failing call on this thread ("" if none). */

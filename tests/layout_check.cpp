@@ -186,10 +186,86 @@ static void run(int sz, const char* name) {
   CHECK(cw_a.worst == 1 && cw_b.worst == 1, "[%s] stage writes conflict\n", name);
 }
 
+// DMA staging + ds_read_b64_tr_b16 operand path of the 16-bit kernels.
+static void run_dma16() {
+  const int KE = 64;  // k per k-tile
+  std::vector<uint16_t> A(BM * KE), B(KE * BN);
+  for (int m = 0; m < BM; ++m)
+    for (int k = 0; k < KE; ++k) A[m * KE + k] = (uint16_t)((m * 7 + k * 3) % 13 + 1);
+  for (int k = 0; k < KE; ++k)
+    for (int n = 0; n < BN; ++n) B[k * BN + n] = (uint16_t)((k * 5 + n * 11) % 17 + 1);
+  std::vector<uint8_t> sa(BM * 128), sb(KE * 256);
+  std::vector<int> ca(sa.size(), 0), cb(sb.size(), 0);
+  for (int w = 0; w < 4; ++w)
+    for (int j = 0; j < 4; ++j) {
+      const int b = dma_block(w, j);
+      for (int i = 0; i < 64; ++i) {
+        const int row = dma_a_row(b, i), c = dma_a_chunk(b, i);
+        const int dst = b * 1024 + 16 * i;
+        CHECK(a_lds_offset(row, c) == dst, "[dma16] A lane %d of block %d lands off-layout\n", i, b);
+        std::memcpy(&sa[dst], &A[row * KE + c * 8], 16);
+        for (int x = 0; x < 16; ++x) ca[dst + x]++;
+        const int kr = dma_b_row(b, i), cc = dma_b_chunk(b, i);
+        CHECK(btr_offset(kr, 8 * cc) == dst, "[dma16] B lane %d of block %d lands off-layout\n", i, b);
+        std::memcpy(&sb[dst], &B[kr * BN + 8 * cc], 16);
+        for (int x = 0; x < 16; ++x) cb[dst + x]++;
+      }
+    }
+  for (size_t i = 0; i < ca.size(); ++i) CHECK(ca[i] == 1 && cb[i] == 1, "[dma16] LDS byte %zu coverage\n", i);
+  Conflicts cr;
+  for (int wave = 0; wave < 4; ++wave) {
+    const int wn = wave & 1;
+    for (int s = 0; s < 4; ++s)
+      for (int nt = 0; nt < 2; ++nt) {
+        const int nb = wn * 64 + nt * 32;
+        uint16_t op[64][8];
+        for (int h = 0; h < 2; ++h) {
+          uint16_t src[64][4];
+          std::vector<int> addrs;
+          for (int l = 0; l < 64; ++l) {
+            const int off = btr_offset(btr_k(s, h, l), btr_n(nb, l));
+            std::memcpy(src[l], &sb[off], 8);
+            addrs.push_back(off);
+            if ((l & 31) == 31) {
+              cr.phase(addrs, 8);
+              addrs.clear();
+            }
+          }
+          for (int l = 0; l < 64; ++l)  // the transpose, as measured on gfx950
+            for (int r = 0; r < 4; ++r) op[l][4 * h + r] = src[16 * (l / 16) + 4 * r + (l % 16) / 4][(l % 16) % 4];
+        }
+        for (int l = 0; l < 64; ++l)
+          for (int e = 0; e < 8; ++e) {
+            const int k = 16 * s + 8 * (l >> 5) + e, n = nb + (l & 31);
+            CHECK(op[l][e] == B[k * BN + n], "[dma16] B operand lane %d elem %d: got %d want %d\n", l, e, op[l][e],
+                  B[k * BN + n]);
+            // the A operand of the same lane covers the same k
+            const int koff = frag_chunk(l, s) * 8;
+            CHECK(koff + e == k, "[dma16] A/B k mismatch lane %d\n", l);
+          }
+      }
+  }
+  std::printf("[dma16] tr-read bank-conflict ways: %d\n", cr.worst);
+  CHECK(cr.worst == 1, "[dma16] tr reads conflict\n");
+}
+
 int main() {
+  run_dma16();
   run(2, "f16/bf16");
   run(1, "fp8");
   run(4, "f32");
+  // tile_of_block: every (row block, column tile) exactly once
+  for (auto rc : std::vector<std::pair<int64_t, int64_t>>{{16, 16}, {8, 256}, {1024, 16}, {2, 3}, {5, 7}, {3, 1}}) {
+    const int64_t R = rc.first, C = rc.second, G = R * C;
+    std::set<std::pair<int64_t, int64_t>> seen2;
+    for (int64_t b = 0; b < G; ++b) {
+      int64_t r, c;
+      tile_of_block(b, G, R, C, &r, &c);
+      CHECK(r >= 0 && r < R && c >= 0 && c < C, "tile_of_block out of range\n");
+      seen2.insert({r, c});
+    }
+    CHECK((int64_t)seen2.size() == G, "tile_of_block not a bijection for %lldx%lld\n", (long long)R, (long long)C);
+  }
   for (int64_t G : {256LL, 16384LL, 8LL, 100LL, 7LL, 2048LL}) {
     std::set<int64_t> s;
     for (int64_t b = 0; b < G; ++b) s.insert(xcd_remap(b, G));

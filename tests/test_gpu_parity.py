@@ -32,7 +32,7 @@ def _check(cfg: ChainConfig, inp: O.ChainInputs, out: torch.Tensor, rows, batche
     for bt in batches:
         logits, probs = O.chain_rows(inp.a[bt], inp.b[bt], rows, inp.scale)
         metrics.append(compare_rows(out_np[bt][rows], probs, logits, cfg.out_dtype,
-                                    label=f"{cfg.name} batch {bt}"))
+                                    label=f"{cfg.name} batch {bt}", in_dtype=cfg.in_dtype))
     check_row_sums(out, cfg.name)
     return metrics
 
@@ -55,8 +55,10 @@ def test_c2_f16_headline(native_lib, path):
     inp = O.make_inputs(cfg, seed=0)
     out = run_chain(inp, cfg.in_dtype, cfg.out_dtype, path=path)
     _check(cfg, inp, out, sample_rows(cfg.m, 48))
-    from welder_typical_chain_amd.chain import read_error_flags
-    assert read_error_flags() == 0
+    from welder_typical_chain_amd.chain import read_diagnostics
+    flags, longest_wait, timeouts = read_diagnostics()
+    print(f"[gpu-case] row-block waits: longest {longest_wait / 100:.1f} us, timeouts {timeouts}")
+    assert flags == 0 and timeouts == 0
 
 
 @needs_gpu
@@ -124,3 +126,38 @@ def test_negative_scale_and_shift_invariance(native_lib):
     inp = O.make_inputs(cfg, seed=11)
     out = run_chain(inp, "f16", "f32")
     _check(cfg, inp, out, np.arange(128))
+
+
+@needs_gpu
+def test_exchange_repeated_launches_and_workspace_reuse(native_lib):
+    """40 exchange launches with changing inputs on one workspace (stale row
+    statistics or counters would show as wrong rows), then the same workspace
+    reused for a smaller shape and back (the counter region must survive)."""
+    import math
+    from welder_typical_chain_amd.chain import (matmul_softmax, new_workspace, read_diagnostics,
+                                                workspace_size)
+    _announce("exchange: 40 launches with changing inputs + workspace reuse across shapes")
+    dev = torch.device("cuda")
+    m = n = 2048
+    k = 1024
+    ws = new_workspace(workspace_size(1, m, n, k, 1, 1) + (1 << 20), dev)
+    out = torch.empty((m, n), dtype=torch.float16, device=dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+    worst = 0.0
+    for it in range(40):
+        a = (torch.randn((m, k), generator=g, device=dev) * (0.5 + it / 20) / math.sqrt(k)).half()
+        b = (torch.randn((k, n), generator=g, device=dev) / math.sqrt(k)).half()
+        matmul_softmax(a, b, out=out, path="exchange", workspace=ws)
+        ref = torch.softmax(a.float() @ b.float(), dim=-1)
+        worst = max(worst, float(((out.float() - ref).abs() / ref).max()))
+        if it in (10, 20):  # a different shape on the same workspace, all paths
+            for path in ("exchange", "split", "unfused"):
+                small = matmul_softmax(a[:200, :64].contiguous(), b[:64, :264].contiguous(),
+                                       path=path, workspace=ws)
+                sref = torch.softmax(a[:200, :64].float() @ b[:64, :264].float(), dim=-1)
+                assert float((small.float() - sref).abs().max()) < 2e-3
+    torch.cuda.synchronize()
+    flags, longest, timeouts = read_diagnostics(ws)
+    print(f"[gpu-case] worst rel err {worst:.3e}; longest wait {longest / 100:.1f} us; timeouts {timeouts}")
+    assert worst < 2e-3 and flags == 0 and timeouts == 0

@@ -96,8 +96,14 @@ def matmul_softmax(a: torch.Tensor, b: torch.Tensor, *, out: torch.Tensor | None
 
 
 def read_error_flags(workspace: torch.Tensor | None = None, clear: bool = True) -> int:
+    """Bit 0 set when a row-block wait of the exchange path timed out."""
+    return read_diagnostics(workspace, clear)[0]
+
+
+def read_diagnostics(workspace: torch.Tensor | None = None, clear: bool = True):
+    """(flags, longest row-block wait in 100 MHz ticks, timed-out waits)."""
     import ctypes
-    flags = ctypes.c_uint32(0)
+    words = (ctypes.c_uint32 * 3)()
     ptr = workspace.data_ptr() if workspace is not None else None
-    _lib.check(_lib.lib().wtc_read_error_flags(ptr, ctypes.byref(flags), int(clear)))
-    return int(flags.value)
+    _lib.check(_lib.lib().wtc_read_error_flags(ptr, words, int(clear)))
+    return int(words[0]), int(words[1]), int(words[2])

@@ -51,18 +51,26 @@ constexpr int BN = 128;
 constexpr int NTHREADS = 256;
 constexpr int A_STAGE_BYTES = BM * kKTileBytes;                  // 16 KiB
 constexpr int STAGE_BYTES = A_STAGE_BYTES + BN * kKTileBytes;    // 32 KiB
-constexpr int RING_BYTES = 2 * STAGE_BYTES;                      // 64 KiB
 constexpr uint32_t kOutOfRange = 0x80000000u;  // buffer offset that reads 0
+
+// 16-bit inputs stream through a 4-stage ring filled by direct-to-LDS loads;
+// fp8 / f32 through a 2-stage ring filled from registers.
+template <int IN_DT> struct Ring {
+  static constexpr bool kDma = IN_DT == DT_F16 || IN_DT == DT_BF16;
+  static constexpr int kStages = kDma ? 4 : 2;
+  static constexpr int kBytes = kStages * STAGE_BYTES;
+};
 
 template <int OUT_DT> struct OutTraits;
 template <> struct OutTraits<DT_F32> { static constexpr int SZ = 4; };
 template <> struct OutTraits<DT_F16> { static constexpr int SZ = 2; };
 template <> struct OutTraits<DT_BF16> { static constexpr int SZ = 2; };
 
-template <int OUT_DT> struct EpiLayout {
+template <int IN_DT, int OUT_DT> struct EpiLayout {
   static constexpr int PITCH = BN * OutTraits<OUT_DT>::SZ + 16;  // staging row pitch
   static constexpr int STAGING = BM * PITCH;
-  static constexpr int UNION = STAGING > RING_BYTES ? STAGING : RING_BYTES;
+  static constexpr int RING = Ring<IN_DT>::kBytes;
+  static constexpr int UNION = STAGING > RING ? STAGING : RING;
   static constexpr int RED_OFF = (UNION + 255) / 256 * 256;
   // redmax[2][BM], redsum[2][BM], factor[BM]  (floats)
   static constexpr int TOTAL = RED_OFF + 5 * BM * 4;
@@ -147,6 +155,74 @@ template <int IN_DT> struct StageRegs {
 };
 
 // -------------------------------------------------------------------------
+// Direct-to-LDS staging (16-bit inputs).  The loads are issued from inline
+// asm with their outstanding count tracked by hand: the compiler would
+// otherwise wait for every load in flight before any LDS read, since it
+// cannot tell the ring stages apart.  Extra loads in flight can only make
+// the compiler's own s_waitcnt more conservative, never unsafe.
+// -------------------------------------------------------------------------
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+#define WTC_LDS __attribute__((address_space(3)))
+
+// Raw buffer descriptor: base, stride 0, num_records = bytes, gfx9 dword3.
+__device__ inline i32x4 raw_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  i32x4 r;
+  r[0] = (int)(uint32_t)a;
+  r[1] = (int)((uint32_t)(a >> 32) & 0xFFFFu);
+  r[2] = (int)bytes;
+  r[3] = 0x00020000;
+  return r;
+}
+
+// 16 bytes per lane into LDS at lds_base + 16*lane.
+__device__ inline void dma16(i32x4 rsrc, uint32_t voff, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(lds_base), "v"(voff), "s"(rsrc)
+               : "memory", "m0");
+}
+
+// Wait until at most N of this wave's direct-to-LDS loads are in flight and
+// its LDS reads are done, then meet the other waves.
+template <int N>
+__device__ inline void wait_loads_barrier() {
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "n"(N) : "memory");
+}
+
+struct DmaTile {
+  i32x4 ra, rb;
+  int64_t row0, n0, M, N, K, lda, ldb;
+};
+
+// One k-tile (A and B, 2 x 16 KiB) into the stage at LDS byte address `stage`.
+// wave_u is the wave index as a scalar.
+__device__ inline void dma_tile16(const DmaTile& d, uint32_t stage, int wave_u, int lane, int kt) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int b = dma_block(wave_u, j);
+    const int64_t row = d.row0 + dma_a_row(b, lane);
+    const int64_t kb = (int64_t)kt * kKTileBytes + dma_a_chunk(b, lane) * kChunkBytes;
+    const bool oka = row < d.M && kb < d.K * 2;
+    dma16(d.ra, oka ? (uint32_t)(row * d.lda + kb) : kOutOfRange, stage + b * 1024);
+    const int64_t k = (int64_t)kt * (kKTileBytes / 2) + dma_b_row(b, lane);
+    const int64_t n = d.n0 + 8 * dma_b_chunk(b, lane);
+    const bool okb = k < d.K && n < d.N;
+    dma16(d.rb, okb ? (uint32_t)(k * d.ldb + n * 2) : kOutOfRange, stage + A_STAGE_BYTES + b * 1024);
+  }
+}
+
+typedef __fp16 h4 __attribute__((__vector_size__(4 * sizeof(__fp16))));
+
+__device__ inline u32x2 tr_read(const uint8_t* p) {
+  const h4 v = __builtin_amdgcn_ds_read_tr16_b64_v4f16((WTC_LDS h4*)(p));
+  return __builtin_bit_cast(u32x2, v);
+}
+
+struct Frags;
+__device__ inline void read_frags_tr(const uint8_t* stage, int lane, int wm, int wn, int s, Frags& f);
+
+// -------------------------------------------------------------------------
 // MFMA over one LDS stage: wave (wm, wn) accumulates its 64x64 block.
 // acc[mt][nt] holds D = B^T A^T for m-subtile mt, n-subtile nt.
 // Fragments of step s+1 are read while the MFMAs of step s issue.
@@ -166,6 +242,24 @@ __device__ inline void read_frags(const uint8_t* stage, int lane, int wm, int wn
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt)
     f.b[nt] = *reinterpret_cast<const u32x4*>(sB + b_lds_offset(kch, wn * 64 + nt * 32 + r, BN));
+}
+
+// 16-bit fragments with B read K-major through the transpose read.
+__device__ inline void read_frags_tr(const uint8_t* stage, int lane, int wm, int wn, int s, Frags& f) {
+  const uint8_t* sA = stage;
+  const uint8_t* sB = stage + A_STAGE_BYTES;
+  const int r = frag_row(lane);
+  const int kch = frag_chunk(lane, s);
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+    f.a[mt] = *reinterpret_cast<const u32x4*>(sA + a_lds_offset(wm * 64 + mt * 32 + r, kch));
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    const int nb = wn * 64 + nt * 32;
+    const u32x2 lo = tr_read(sB + btr_offset(btr_k(s, 0, lane), btr_n(nb, lane)));
+    const u32x2 hi = tr_read(sB + btr_offset(btr_k(s, 1, lane), btr_n(nb, lane)));
+    f.b[nt] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+  }
 }
 
 template <int IN_DT>
@@ -229,6 +323,19 @@ __device__ inline void mma_stage(const uint8_t* stage, int lane, int wm, int wn,
   }
 }
 
+template <int IN_DT>
+__device__ inline void mma_stage_tr(const uint8_t* stage, int lane, int wm, int wn,
+                                    f32x16 (&acc)[2][2]) {
+  constexpr int S = kChunksPerKTile / 2;
+  Frags f[2];
+  read_frags_tr(stage, lane, wm, wn, 0, f[0]);
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    if (s + 1 < S) read_frags_tr(stage, lane, wm, wn, s + 1, f[(s + 1) & 1]);
+    mma_step<IN_DT>(f[s & 1], acc);
+  }
+}
+
 // -------------------------------------------------------------------------
 // Output conversion
 // -------------------------------------------------------------------------
@@ -272,33 +379,50 @@ __device__ inline float2 load_stat(const float2* p) {
 }
 
 // Arrival of one tile at its row block's counter (called by one thread after
-// the tile's statistics are stored and released).  Returns once every tile
-// of the row block has arrived, or after spin_ticks of the 100 MHz clock (then
-// err gets bit 0 and the tile goes on with what it sees, so the kernel always
-// drains).  The last arriver resets the counter and bumps the generation
-// word, so the protocol keeps no per-launch state and survives graph replay.
-// The poll itself is a relaxed load: no cache maintenance inside the loop.
-__device__ inline void rowblock_barrier(uint32_t* cnt_gen, int nT, uint32_t* err,
+// the tile's statistics are stored).  Returns once every tile of the row
+// block has arrived, or after spin_ticks of the 100 MHz clock (then err gets
+// bit 0 and the tile goes on with what it sees, so the kernel always drains).
+// The last arriver resets the counter and bumps the generation word, so the
+// protocol keeps no per-launch state and survives graph replay.
+//
+// Memory ordering without cache maintenance: every word that crosses
+// workgroups here (statistics, counter, generation) is read and written only
+// with agent-scope atomics, which are coherent across the XCDs' L2s.  The
+// order that matters -- a tile's statistics are in place before its arrival
+// is counted, and are read only after the generation moved -- is enforced by
+// waiting for the statistics stores to complete (s_waitcnt) before the
+// counter RMW, and by issuing the statistics loads after the poll returned.
+// Agent-scope release/acquire fences would write back / invalidate the whole
+// L2 of the XCD, which costs far more than the exchange itself.
+//
+// The counter and the generation word of a row block sit in cache lines of
+// their own (kSyncWords apart per row block): polls of one row block do not
+// contend with the arrivals of another, nor with their own counter.
+// g0 is the generation word as read at kernel start (it cannot change before
+// this tile arrives, so reading it early keeps it off the critical path).
+__device__ inline void rowblock_barrier(uint32_t* cnt_gen, uint32_t g0, int nT, uint32_t* err,
                                         uint64_t spin_ticks) {
   uint32_t* cnt = cnt_gen;
-  uint32_t* gen = cnt_gen + 1;
-  const uint32_t g0 = __hip_atomic_load(gen, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
-  const uint32_t old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+  uint32_t* gen = cnt_gen + kSyncWords / 2;
+  const uint32_t old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   if (old == (uint32_t)(nT - 1)) {
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "agent");
     __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_fetch_add(gen, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_fetch_add(gen, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
   }
   const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+  uint64_t waited = 0;
   while (__hip_atomic_load(gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == g0) {
-    __builtin_amdgcn_s_sleep(2);
-    if (__builtin_amdgcn_s_memrealtime() - t0 > spin_ticks) {
+    __builtin_amdgcn_s_sleep(8);
+    waited = __builtin_amdgcn_s_memrealtime() - t0;
+    if (waited > spin_ticks) {
       __hip_atomic_fetch_or(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_fetch_add(err + 2, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       break;
     }
   }
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  const uint32_t w32 = waited > 0xFFFFFFFFull ? 0xFFFFFFFFu : (uint32_t)waited;
+  __hip_atomic_fetch_max(err + 1, w32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // -------------------------------------------------------------------------
@@ -307,7 +431,7 @@ __device__ inline void rowblock_barrier(uint32_t* cnt_gen, int nT, uint32_t* err
 template <int IN_DT, int OUT_DT, int EPI, int PF>
 __global__ void __launch_bounds__(NTHREADS, 1)
 chain_tile_kernel(const ChainParams p) {
-  using L = EpiLayout<OUT_DT>;
+  using L = EpiLayout<IN_DT, OUT_DT>;
   __shared__ __attribute__((aligned(16))) uint8_t smem[L::TOTAL];
   float* redmax = reinterpret_cast<float*>(smem + L::RED_OFF);
   float* redsum = redmax + 2 * BM;
@@ -318,9 +442,8 @@ chain_tile_kernel(const ChainParams p) {
   const int wave = t >> 6;
   const int wm = wave >> 1, wn = wave & 1;
 
-  const int64_t tile = xcd_remap(blockIdx.x, gridDim.x);
-  const int64_t nt = tile % p.nT;
-  const int64_t rbg = tile / p.nT;  // row block across batches
+  int64_t rbg, nt;  // row block across batches, column tile
+  tile_of_block(blockIdx.x, gridDim.x, (int64_t)gridDim.x / p.nT, p.nT, &rbg, &nt);
   const int64_t bt = rbg / p.nRB;
   const int64_t rb = rbg % p.nRB;
   const int64_t row0 = rb * BM;
@@ -339,6 +462,12 @@ chain_tile_kernel(const ChainParams p) {
   tl.ldb = p.ldb_bytes;
   uint8_t* o_base = p.out + bt * p.o_bstride;
   const int nk = (int)((p.K * SZ + kKTileBytes - 1) / kKTileBytes);
+  uint32_t gen0 = 0;
+  if constexpr (EPI == kEpiExchange) {
+    if (t == 0)
+      gen0 = __hip_atomic_load(p.sync + kSyncWords * rbg + kSyncWords / 2, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+  }
 
   f32x16 acc[2][2];
 #pragma unroll
@@ -348,13 +477,41 @@ chain_tile_kernel(const ChainParams p) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-  // ---- main loop: PF k-tiles in registers, 2-stage LDS ring --------------
-  // k-tile j lives in R[j % PF] and is loaded PF-1 iterations before the
-  // iteration that moves it to LDS.  Loads past the last k-tile read zeros
-  // (buffer range check), so the steady-state loop issues every load and
-  // store unconditionally and the compiler's count of outstanding loads stays
-  // exact; the last nk % PF k-tiles run in a guarded tail.
-  if (nk > 0) {
+  if constexpr (Ring<IN_DT>::kDma) {
+    // ---- main loop, 16-bit: 4-stage ring of direct-to-LDS loads -----------
+    // k-tile j goes to stage j % 4, issued three iterations before use; each
+    // wave issues 8 loads per k-tile, so "k-tile kt landed" is vmcnt <= 16.
+    // Loads past the last k-tile read zeros into stages never read again.
+    constexpr int S = Ring<IN_DT>::kStages;
+    DmaTile d;
+    d.ra = raw_rsrc(p.a + bt * p.a_bstride, (uint32_t)p.a_bstride);
+    d.rb = raw_rsrc(p.b + bt * p.b_bstride, (uint32_t)p.b_bstride);
+    d.row0 = row0;
+    d.n0 = n0;
+    d.M = p.M;
+    d.N = p.N;
+    d.K = p.K;
+    d.lda = p.lda_bytes;
+    d.ldb = p.ldb_bytes;
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(WTC_LDS uint8_t*)smem;
+    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+    if (nk > 0) {
+#pragma unroll
+      for (int q = 0; q < S - 1; ++q) dma_tile16(d, lds0 + q * STAGE_BYTES, wave_u, lane, q);
+      for (int kt = 0; kt < nk; ++kt) {
+        wait_loads_barrier<8 * (S - 2)>();
+        dma_tile16(d, lds0 + ((kt + S - 1) % S) * STAGE_BYTES, wave_u, lane, kt + S - 1);
+        mma_stage_tr<IN_DT>(smem + (kt % S) * STAGE_BYTES, lane, wm, wn, acc);
+      }
+      wait_loads_barrier<0>();
+    }
+  } else if (nk > 0) {
+    // ---- main loop, fp8 / f32: PF k-tiles in registers, 2-stage LDS ring --
+    // k-tile j lives in R[j % PF] and is loaded PF-1 iterations before the
+    // iteration that moves it to LDS.  Loads past the last k-tile read zeros
+    // (buffer range check), so the steady-state loop issues every load and
+    // store unconditionally and the compiler's count of outstanding loads
+    // stays exact; the last nk % PF k-tiles run in a guarded tail.
     StageRegs<IN_DT> R[PF];
 #pragma unroll
     for (int q = 0; q < PF; ++q) R[q].load(tl, q, t);
@@ -438,18 +595,37 @@ chain_tile_kernel(const ChainParams p) {
       factor[t] = 1.0f;
     }
     if constexpr (EPI == kEpiExchange) {
-      if (t < BM) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+      // statistics stores complete before this tile is counted
+      if (t < BM) __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
-      if (t == 0) rowblock_barrier(p.sync + 2 * rbg, p.nT, p.err, p.spin_ticks);
+      if (t == 0) rowblock_barrier(p.sync + kSyncWords * rbg, gen0, p.nT, p.err, p.spin_ticks);
+      __syncthreads();
+      // Every thread fetches its share of the row block's BM x nT statistics
+      // (independent loads, one round trip), parks them in LDS (the ring is
+      // free now), then one thread per row merges its nT pairs.
+      float2* stats = reinterpret_cast<float2*>(smem);
+      const float2* st = p.partial + rbg * BM * p.nT;
+      const int total = BM * p.nT;
+      for (int i0 = 0; i0 < total; i0 += 8 * NTHREADS) {
+        float2 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int i = i0 + u * NTHREADS + t;
+          v[u] = i < total ? load_stat(st + i) : make_float2(-INFINITY, 0.0f);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int i = i0 + u * NTHREADS + t;
+          if (i < total) stats[i] = v[u];
+        }
+      }
       __syncthreads();
       if (t < BM) {
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-        const float2* st = p.partial + (rbg * BM + t) * p.nT;
         float gm = -INFINITY, gs = 0.0f;
         for (int q = 0; q < p.nT; ++q) {  // online merge of (max, sum) pairs
-          const float2 s = load_stat(st + q);
-          const float nm = fmaxf(gm, s.x);
-          gs = gs * __builtin_amdgcn_exp2f(gm - nm) + s.y * __builtin_amdgcn_exp2f(s.x - nm);
+          const float2 s2 = stats[t * p.nT + q];
+          const float nm = fmaxf(gm, s2.x);
+          gs = gs * __builtin_amdgcn_exp2f(gm - nm) + s2.y * __builtin_amdgcn_exp2f(s2.x - nm);
           gm = nm;
         }
         const float tm = fmaxf(redmax[t], redmax[BM + t]);
@@ -618,11 +794,22 @@ const void* rescale_kernel_symbol(int out_dt) {
 
 const void* zero_kernel_symbol() { return reinterpret_cast<const void*>(&zero_words_kernel); }
 
-int chain_kernel_lds_bytes(int out_dt) {
+template <int IN_DT>
+static int lds_bytes_for(int out_dt) {
   switch (out_dt) {
-    case DT_F32: return EpiLayout<DT_F32>::TOTAL;
-    case DT_F16: return EpiLayout<DT_F16>::TOTAL;
-    case DT_BF16: return EpiLayout<DT_BF16>::TOTAL;
+    case DT_F32: return EpiLayout<IN_DT, DT_F32>::TOTAL;
+    case DT_F16: return EpiLayout<IN_DT, DT_F16>::TOTAL;
+    case DT_BF16: return EpiLayout<IN_DT, DT_BF16>::TOTAL;
+  }
+  return 0;
+}
+
+int chain_kernel_lds_bytes(int in_dt, int out_dt) {
+  switch (in_dt) {
+    case DT_F32: return lds_bytes_for<DT_F32>(out_dt);
+    case DT_F16: return lds_bytes_for<DT_F16>(out_dt);
+    case DT_BF16: return lds_bytes_for<DT_BF16>(out_dt);
+    case DT_FP8: return lds_bytes_for<DT_FP8>(out_dt);
   }
   return 0;
 }

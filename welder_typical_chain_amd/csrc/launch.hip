@@ -21,6 +21,7 @@ constexpr int kTile = 128;            // BM = BN of chain_tile_kernel
 constexpr int kThreads = 256;
 constexpr int kRescaleRowsPerWg = 4;  // rescale_rows_kernel
 constexpr int kRescaleMaxTiles = 512;
+constexpr int kExchangeMaxTiles = 64;        // row statistics staged in the 64 KiB LDS ring
 constexpr uint64_t kSpinTicks = 200000000ull;  // 2 s of the 100 MHz clock
 constexpr int kMaxDevices = 64;
 
@@ -37,11 +38,17 @@ int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
 bool valid_in(int dt) { return dt == DT_F32 || dt == DT_F16 || dt == DT_BF16 || dt == DT_FP8; }
 bool valid_out(int dt) { return dt == DT_F32 || dt == DT_F16 || dt == DT_BF16; }
 
-// Workspace layout (bytes):
-//   [0, 256)              error flags (u32 at 0)
-//   [256, +sync)          row-block counter/generation pairs
-//   [.., +partial)        per-tile row statistics, float2 [rows_pad][nT]
-//   [.., +logits)         unfused path only: f32 logits, row max, row sum
+// Workspace layout (bytes).  The counter region sits at a fixed place with a
+// fixed size, so a workspace reused across problem shapes never has one
+// call's statistics or logits land on another call's counters (the counters
+// are zeroed once and left at zero by every exchange launch).
+//   [0, 256)                       diagnostic words (flags, longest wait, timeouts)
+//   [256, 256 + kSyncRegion)       row-block counter / generation lines
+//   [.., +partial)                 per-tile row statistics, float2 [rows_pad][nT]
+//   [.., +logits)                  unfused path only: f32 logits, row max, row sum
+constexpr int64_t kMaxSyncRowBlocks = 512;
+constexpr int64_t kSyncRegion = kMaxSyncRowBlocks * kSyncWords * 4;
+
 struct WsLayout {
   int64_t sync_off, sync_bytes;
   int64_t partial_off, partial_bytes;
@@ -54,7 +61,7 @@ WsLayout ws_layout(int64_t batch, int64_t m, int64_t n, int path) {
   const int64_t nRB = ceil_div(m, kTile), nT = ceil_div(n, kTile);
   const int64_t rbs = batch * nRB;
   w.sync_off = 256;
-  w.sync_bytes = align256(rbs * 2 * 4);
+  w.sync_bytes = kSyncRegion;
   w.partial_off = w.sync_off + w.sync_bytes;
   w.partial_bytes = align256(rbs * kTile * nT * 8);
   w.total = w.partial_off + w.partial_bytes;
@@ -94,11 +101,16 @@ int plan_impl(int64_t batch, int64_t m, int64_t n, int64_t k, int in_dt, int out
   const int64_t tiles = batch * ceil_div(m, kTile) * ceil_div(n, kTile);
   const int64_t capacity = (int64_t)cu_count * (int64_t)wg_per_cu;
   int p = path;
-  if (p == WTC_PATH_AUTO) p = (tiles <= capacity) ? WTC_PATH_EXCHANGE : WTC_PATH_SPLIT;
+  const int64_t nT = ceil_div(n, kTile);
+  const int64_t rbs = batch * ceil_div(m, kTile);
+  const bool fits = tiles <= capacity && nT <= kExchangeMaxTiles && rbs <= kMaxSyncRowBlocks;
+  if (p == WTC_PATH_AUTO) p = fits ? WTC_PATH_EXCHANGE : WTC_PATH_SPLIT;
   if (p == WTC_PATH_EXCHANGE && tiles > capacity)
     return fail(WTC_ERR_UNSUPPORTED,
                 "exchange path needs every tile co-resident: " + std::to_string(tiles) +
                     " tiles > " + std::to_string(capacity) + " resident workgroups");
+  if (p == WTC_PATH_EXCHANGE && (nT > kExchangeMaxTiles || rbs > kMaxSyncRowBlocks))
+    return fail(WTC_ERR_UNSUPPORTED, "exchange path supports n <= 8192 and <= 512 row blocks");
   if (p == WTC_PATH_SPLIT && ceil_div(n, kTile) > kRescaleMaxTiles)
     return fail(WTC_ERR_UNSUPPORTED, "split path supports n <= 65536");
   if (tiles > 0x7FFFFFFFll) return fail(WTC_ERR_UNSUPPORTED, "too many tiles for one grid");
@@ -128,8 +140,8 @@ DeviceState g_dev[kMaxDevices];
 
 // Dynamic LDS added to the exchange kernel so that no CU holds two of its
 // workgroups (spreads a grid of <= CU-count tiles over all CUs).
-int exchange_lds_pad(int out_dt) {
-  const int stat = chain_kernel_lds_bytes(out_dt);
+int exchange_lds_pad(int in_dt, int out_dt) {
+  const int stat = chain_kernel_lds_bytes(in_dt, out_dt);
   const int want = 80 * 1024 + 1024;
   return stat >= want ? 0 : want - stat;
 }
@@ -144,7 +156,7 @@ int device_state(int dev, DeviceState** out) {
     for (int i = 0; i < 4; ++i)
       for (int o = 0; o < 3; ++o) {
         const void* fn = chain_kernel_symbol(i, o, kEpiExchange);
-        const int pad = exchange_lds_pad(o);
+        const int pad = exchange_lds_pad(i, o);
         HIP_TRY(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, pad));
         int nb = 0;
         HIP_TRY(hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, fn, kThreads, pad));
@@ -229,16 +241,16 @@ int wtc_read_error_flags(void* workspace, uint32_t* flags, int clear) {
     HIP_TRY(hipGetDevice(&dev));
     std::lock_guard<std::mutex> lk(g_mu);
     if (dev < 0 || dev >= kMaxDevices || !g_dev[dev].ws) {
-      *flags = 0;
+      flags[0] = flags[1] = flags[2] = 0;
       return WTC_OK;
     }
     ws = g_dev[dev].ws;
   }
   HIP_TRY(hipDeviceSynchronize());
-  HIP_TRY(hipMemcpy(flags, ws, 4, hipMemcpyDeviceToHost));
+  HIP_TRY(hipMemcpy(flags, ws, 3 * sizeof(uint32_t), hipMemcpyDeviceToHost));
   if (clear) {
-    uint32_t zero = 0;
-    HIP_TRY(hipMemcpy(ws, &zero, 4, hipMemcpyHostToDevice));
+    const uint32_t zero[3] = {0, 0, 0};
+    HIP_TRY(hipMemcpy(ws, zero, sizeof zero, hipMemcpyHostToDevice));
   }
   return WTC_OK;
 }
@@ -311,7 +323,7 @@ int wtc_matmul_softmax(const void* a, const void* b, void* out, int64_t batch, i
 
   if (chosen == WTC_PATH_EXCHANGE) {
     return launch_chain(chain_kernel_symbol(in_dtype, out_dtype, kEpiExchange), grid,
-                        exchange_lds_pad(out_dtype), p, stream);
+                        exchange_lds_pad(in_dtype, out_dtype), p, stream);
   }
   if (chosen == WTC_PATH_SPLIT) {
     rc = launch_chain(chain_kernel_symbol(in_dtype, out_dtype, kEpiSplit), grid, 0, p, stream);

@@ -107,13 +107,67 @@ WTC_HD uint32_t b_unit_word(const Words& rw, int sz, int c, int w) {
   return rw(b_src_word(4, w, c));
 }
 
+// ---- direct-to-LDS (DMA) staging of 16-bit k-tiles --------------------------
+// A buffer_load ... lds instruction writes lane i's 16 bytes at
+// LDS base + 16*i: each wave instruction fills one contiguous 1 KiB block, so
+// the swizzles are realised by choosing which global chunk each lane fetches.
+// Wave w issues instructions j = 0..3 for A and for B: block b = 4w + j.
+WTC_HD constexpr int dma_block(int wave, int j) { return 4 * wave + j; }
+// A block b = rows 8b..8b+7 of the A stage; lane i lands in row 8b + i/8,
+// slot i%8, which a_lds_offset assigns to chunk slot ^ ((row>>1)&7).
+WTC_HD constexpr int dma_a_row(int b, int lane) { return 8 * b + (lane >> 3); }
+WTC_HD constexpr int dma_a_chunk(int b, int lane) {
+  return (lane & 7) ^ ((dma_a_row(b, lane) >> 1) & 7);
+}
+// B stays K-major ([k][n], 256 bytes per k-row for BN = 128 16-bit columns)
+// with 16-byte chunks XOR-swizzled by k%4: element (k, n) lives at
+// btr_offset(k, n).  B block b = k-rows 4b..4b+3; lane i lands in row
+// 4b + i/16, slot i%16, which holds chunk slot ^ 4*(row%4).
+WTC_HD constexpr int btr_offset(int k, int n) {
+  return k * 256 + ((((n >> 3) ^ ((k & 3) << 2)) & 15) << 4) + (n & 7) * 2;
+}
+WTC_HD constexpr int dma_b_row(int b, int lane) { return 4 * b + (lane >> 4); }
+WTC_HD constexpr int dma_b_chunk(int b, int lane) {
+  return (lane & 15) ^ ((dma_b_row(b, lane) & 3) << 2);
+}
+// The B operand is read with ds_read_b64_tr_b16: within each group of 16
+// lanes the 4 x 16 matrix formed by lanes 4r..4r+3 (row r, 4 elements each)
+// is transposed, so lane i receives column i: element r of its result is
+// element i%4 of lane 4r + i/4.  For MFMA k-step s, n-subtile base nb and
+// half h (k-quad), lane l supplies the address of (btr_k, btr_n) and gets
+// B[16s + 8(l/32) + 4h + r][nb + l%32] for r = 0..3: with h = 0, 1 that is
+// the same 8 consecutive k the A fragment of lane l holds (frag_chunk).
+WTC_HD constexpr int btr_k(int s, int h, int lane) {
+  return 16 * s + 8 * (lane >> 5) + 4 * h + ((lane & 15) >> 2);
+}
+WTC_HD constexpr int btr_n(int nb, int lane) { return nb + 16 * ((lane >> 4) & 1) + 4 * (lane & 3); }
+
 // ---- workgroup -> tile ------------------------------------------------------
 // Workgroups are dispatched round-robin over the 8 XCDs (blockIdx % 8).
-// Remap so that XCD x receives the contiguous tile range
-// [x*G/8, (x+1)*G/8): the tiles of a row block (consecutive ids) then share
-// one XCD's L2 and their row-statistics exchange stays on that XCD.
+// tile_of_block() first gives XCD x the contiguous range of logical ids
+// [x*G/8, (x+1)*G/8), then maps logical ids to (row block, column tile) in
+// groups of kGroupRows row blocks walked column-major, so the tiles one XCD
+// holds at a time form a compact 2-D block: with 16x16 tiles and 32 per XCD,
+// 4 row blocks x 8 column tiles (3 MiB of operands for a K=1024 f16 chain
+// instead of 4.5 MiB for 2 full row blocks), which is what its L2 has to
+// fetch over the fabric.
+constexpr int kGroupRows = 4;
+
 WTC_HD constexpr int64_t xcd_remap(int64_t b, int64_t G) {
   return (G % 8 == 0) ? (b % 8) * (G / 8) + b / 8 : b;
+}
+
+// rows = row blocks (over all batches), cols = column tiles per row block.
+WTC_HD void tile_of_block(int64_t b, int64_t G, int64_t rows, int64_t cols,
+                                 int64_t* row, int64_t* col) {
+  const int64_t t = xcd_remap(b, G);
+  const int64_t per_group = (int64_t)kGroupRows * cols;
+  const int64_t group = t / per_group;
+  const int64_t first = group * kGroupRows;
+  const int64_t in_group = (rows - first) < kGroupRows ? (rows - first) : kGroupRows;
+  const int64_t r = t - group * per_group;
+  *row = first + r % in_group;
+  *col = r / in_group;
 }
 
 } // namespace wtc

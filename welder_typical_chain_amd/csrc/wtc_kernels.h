@@ -10,6 +10,10 @@ namespace wtc {
 
 enum : int { kEpiExchange = 0, kEpiSplit = 1, kEpiLogits = 2 };
 
+// 32-bit words of workspace per row block for the exchange counter (word 0)
+// and generation (word kSyncWords/2): 256 bytes, two cache lines.
+constexpr int kSyncWords = 64;
+
 struct ChainParams {
   const uint8_t* a;
   const uint8_t* b;
@@ -22,15 +26,16 @@ struct ChainParams {
   int nRB;          // row blocks (of 128 rows) per batch
   int nT;           // column tiles (of 128 columns) per row block
   float2* partial;  // [batch*nRB*128][nT] per-tile row (max, sumexp), log2 domain
-  uint32_t* sync;   // [batch*nRB][2] row-block counter and generation
-  uint32_t* err;    // bit 0: a row-block wait timed out
+  uint32_t* sync;   // [batch*nRB][kSyncWords] row-block counter and generation
+  uint32_t* err;    // [0] bit 0: a row-block wait timed out; [1] longest wait
+                    // (100 MHz ticks); [2] number of timed-out waits
   uint64_t spin_ticks;  // row-block wait limit, 100 MHz ticks
 };
 
 const void* chain_kernel_symbol(int in_dt, int out_dt, int epi);
 const void* rescale_kernel_symbol(int out_dt);
 const void* zero_kernel_symbol();
-int chain_kernel_lds_bytes(int out_dt);
+int chain_kernel_lds_bytes(int in_dt, int out_dt);
 
 // Unfused five-kernel baseline (matmul, row max, exp, row sum, divide).
 const void* rowmax_kernel_symbol();
