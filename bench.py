@@ -40,6 +40,9 @@ def parse():
     ap.add_argument("--path", default="auto", choices=["auto", "exchange", "split", "unfused"])
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="budget of the cpu_baseline sample (0 disables it)")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="before the timed steps, run plain device copies of this many MiB "
+                         "(the byte-count calibration for rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     return ap.parse_args()
 
 
@@ -94,6 +97,15 @@ def main():
 
     def step():
         matmul_softmax(a, b, out=out, path=args.path, workspace=ws)
+
+    if args.copy_probe_mib > 0:
+        n_el = args.copy_probe_mib * (1 << 20) // 4
+        src = torch.ones(n_el, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     for _ in range(args.warmup):
         step()
