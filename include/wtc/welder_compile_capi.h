@@ -13,7 +13,12 @@
  *   04.kernel.plan.json       kernel variant, path, grid / block / LDS
  *   05.out.hip.launch.json    the runnable artefact: library, C entry point
  *                             (wtc_matmul_softmax) and its arguments
- *   kernel_report.txt         resource summary of the selected kernels
+ *   05.out.gfx950.hsaco       the gfx950 device code object of the chain
+ *                             kernels (plus 05.out.rows.gfx950.hsaco for the
+ *                             unfused path's row kernels)
+ *   kernel_report.txt         key=value artifact report (kernel count, MFMA /
+ *                             LDS-DMA / scratch instruction counts, spills)
+ *                             and one line per kernel (registers, LDS)
  * workgroup_pass_plugin_path and welder_compiler_bin_path are accepted and
  * ignored (no MLIR pass plugin or external compiler exists in this build).
  * fused != 0 selects the fused kernel (exchange or split path), fused == 0

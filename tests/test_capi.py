@@ -1,0 +1,253 @@
+"""CPU tests of the C-ABI library: exports, launch planning, argument errors,
+and the compile / solver entry points on chain MLIR files.  Nothing here
+launches a kernel (no GPU in this container)."""
+from __future__ import annotations
+
+import ctypes
+import json
+import re
+from pathlib import Path
+
+import pytest
+
+from welder_typical_chain_amd import _lib
+from welder_typical_chain_amd.chain_mlir import chain_mlir
+from welder_typical_chain_amd.configs import CONFIGS, ChainConfig
+
+ROOT = Path(__file__).resolve().parents[1]
+PKG = ROOT / "welder_typical_chain_amd"
+REF_MLIR = Path("/root/reference/mlir")
+
+
+def declared_functions() -> set[str]:
+    """Every function the public headers declare."""
+    names = set()
+    for h in (ROOT / "include" / "wtc").glob("*.h"):
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        names |= set(re.findall(r"\b((?:wtc|welder)_\w+)\s*\(", text))
+    return names
+
+
+@pytest.fixture(scope="module")
+def L(native_lib):
+    return _lib.lib()
+
+
+def test_every_declared_symbol_is_exported(L):
+    names = declared_functions()
+    assert {"wtc_matmul_softmax", "welder_compile_typical_chain_to_nvvm",
+            "welder_solver_solve_typical_chain"} <= names
+    for n in sorted(names):
+        assert hasattr(L, n), f"{n} declared in include/wtc but not exported"
+    assert names <= set(_lib.SIGNATURES), "ctypes prototypes missing for some declarations"
+
+
+def test_reference_named_libraries():
+    comp = ctypes.CDLL(str(PKG / "libwelder-compile-capi.so"))
+    assert hasattr(comp, "welder_compile_typical_chain_to_nvvm")
+    solver = ctypes.CDLL(str(PKG / "libwelder-solver-capi.so"))
+    assert hasattr(solver, "welder_solver_solve_typical_chain")
+
+
+def test_version(L):
+    assert b"gfx950" in L.wtc_version()
+
+
+def plan(L, batch, m, n, k, i, o, path, cu=256, wg=1):
+    grid, ws = ctypes.c_int64(), ctypes.c_int64()
+    chosen = ctypes.c_int()
+    rc = L.wtc_plan(batch, m, n, k, i, o, path, cu, wg, ctypes.byref(grid), ctypes.byref(chosen),
+                    ctypes.byref(ws))
+    return rc, grid.value, chosen.value, ws.value
+
+
+def test_plan_headline_and_configs(L):
+    # C2: 16 x 16 tiles, one per CU -> one-launch exchange path
+    rc, grid, path, ws = plan(L, 1, 2048, 2048, 1024, _lib.DTYPE_F16, _lib.DTYPE_F16, _lib.PATH_AUTO)
+    assert (rc, grid, path) == (0, 256, _lib.PATH_EXCHANGE)
+    assert ws == L.wtc_matmul_softmax_workspace_size(1, 2048, 2048, 1024, 1, 1, 0)
+    assert ws >= 256 + 512 * 256 + 2048 * 16 * 8
+    # C3: 64 x 256 tiles do not fit at once -> split
+    rc, grid, path, _ = plan(L, 64, 2048, 2048, 128, 1, 1, _lib.PATH_AUTO)
+    assert (rc, grid, path) == (0, 64 * 256, _lib.PATH_SPLIT)
+    # C4: 8 x 256 tiles, 256 column tiles per row -> split
+    rc, grid, path, _ = plan(L, 1, 1024, 32768, 4096, _lib.DTYPE_BF16, 1, _lib.PATH_AUTO)
+    assert (rc, grid, path) == (0, 8 * 256, _lib.PATH_SPLIT)
+    # forcing the exchange path where it cannot be co-resident is refused
+    rc, *_ = plan(L, 1, 1024, 32768, 4096, _lib.DTYPE_BF16, 1, _lib.PATH_EXCHANGE)
+    assert rc == _lib.WTC_ERR_UNSUPPORTED and b"co-resident" in L.wtc_last_error()
+    # ragged: 200 x 264 -> 2 x 3 tiles
+    rc, grid, path, _ = plan(L, 1, 200, 264, 72, 1, 1, _lib.PATH_AUTO)
+    assert (rc, grid, path) == (0, 6, _lib.PATH_EXCHANGE)
+    # unfused needs room for the f32 logits
+    _, _, _, ws_u = plan(L, 1, 2048, 2048, 1024, 1, 1, _lib.PATH_UNFUSED)
+    assert ws_u >= ws + 2048 * 2048 * 4
+
+
+@pytest.mark.parametrize("args,code", [
+    ((1, 128, 128, 4, 1, 1, 0), _lib.WTC_ERR_ARG),     # k*2 bytes not a multiple of 16
+    ((1, 128, 100, 64, 1, 1, 0), _lib.WTC_ERR_ARG),    # n not a multiple of 8
+    ((1, -1, 128, 64, 1, 1, 0), _lib.WTC_ERR_ARG),
+    ((1, 128, 128, 64, 7, 1, 0), _lib.WTC_ERR_ARG),    # in dtype
+    ((1, 128, 128, 64, 1, 3, 0), _lib.WTC_ERR_ARG),    # fp8 output is not offered
+    ((1, 128, 128, 64, 1, 1, 9), _lib.WTC_ERR_ARG),    # path
+])
+def test_plan_rejects_bad_arguments(L, args, code):
+    rc, *_ = plan(L, *args)
+    assert rc == code
+    assert L.wtc_last_error()
+    assert L.wtc_matmul_softmax_workspace_size(*args) < 0
+
+
+def test_launch_argument_errors_without_gpu(L):
+    # argument checks come before any HIP call
+    rc = L.wtc_matmul_softmax(None, None, None, 1, 128, 128, 4, 1, 1, 1.0, 1.0, 1.0, 0, None, 0, None)
+    assert rc == _lib.WTC_ERR_ARG
+    # nothing to do: returns OK without touching a device
+    rc = L.wtc_matmul_softmax(None, None, None, 1, 0, 128, 64, 1, 1, 1.0, 1.0, 1.0, 0, None, 0, None)
+    assert rc == _lib.WTC_OK
+    assert L.wtc_read_error_flags(None, None, 1) == _lib.WTC_ERR_ARG
+
+
+# ---- compile / solver entry points --------------------------------------------
+
+def write_chain(tmp_path: Path, cfg: ChainConfig, **kw) -> Path:
+    p = tmp_path / f"{cfg.name.lower()}{'_named' if kw.get('named_softmax') else ''}.mlir"
+    p.write_text(chain_mlir(cfg, **kw))
+    return p
+
+
+def solve(L, path: Path, out: Path, errsize=4096):
+    tiles = [ctypes.c_int64() for _ in range(5)]
+    err = ctypes.create_string_buffer(errsize) if errsize else None
+    rc = L.welder_solver_solve_typical_chain(
+        str(path).encode(), str(out / "best_summary.json").encode(),
+        str(out / "candidates.tsv").encode(), 1, 0, *[ctypes.byref(t) for t in tiles], err, errsize)
+    return rc, [t.value for t in tiles], (err.value if err is not None else b"")
+
+
+def compile_chain(L, path: Path, out: Path, tiles, fused=1, errsize=4096):
+    err = ctypes.create_string_buffer(errsize)
+    rc = L.welder_compile_typical_chain_to_nvvm(str(path).encode(), str(out).encode(), b"", b"",
+                                                *tiles, 1, fused, 0, err, errsize)
+    return rc, err.value
+
+
+EXPECT = {  # config -> (tile_k, path chosen for the fused kernel)
+    "C1": (32, "exchange"), "C2": (64, "exchange"), "C3": (64, "split"),
+    "C4": (64, "split"), "C5": (128, "split"),
+}
+
+
+@pytest.mark.parametrize("name", sorted(EXPECT))
+@pytest.mark.parametrize("named", [False, True])
+def test_solver_and_compile_per_config(L, tmp_path, name, named):
+    cfg = CONFIGS[name]
+    src = write_chain(tmp_path, cfg, named_softmax=named)
+    rc, tiles, err = solve(L, src, tmp_path)
+    assert rc == 0, err
+    tile_k, path = EXPECT[name]
+    assert tiles == [128, 128, tile_k, 2, 32]
+    summary = json.loads((tmp_path / "best_summary.json").read_text())
+    assert {k: summary["problem"][k] for k in "mnk"} == {"m": cfg.m, "n": cfg.n, "k": cfg.k}
+    assert {"smemBytes", "numSM", "warpSize", "elementBytes"} <= set(summary["arch"])
+    assert {"tileM", "tileN", "tileK", "threadTileM", "threadTileN", "score", "estimatedLatency",
+            "profiledMs", "bytesCut"} <= set(summary["best"])
+    rows = (tmp_path / "candidates.tsv").read_text().strip().split("\n")
+    assert rows[0].split("\t") == ["rank", "tileM", "tileN", "tileK", "threadTileM", "threadTileN",
+                                   "score", "estimatedLatency", "profiledMs", "bytesA", "bytesB",
+                                   "bytesC", "bytesCut"]
+    assert all(len(r.split("\t")) == 13 for r in rows[1:]) and len(rows) >= 2
+    # the reference reads tiles from JSON with a first-match regex (Search.cpp:12-20)
+    text = (tmp_path / "best_summary.json").read_text()
+    got = [int(re.search(rf'"{k}"\s*:\s*(-?[0-9]+)', text).group(1))
+           for k in ("tileM", "tileN", "tileK", "threadTileM", "threadTileN")]
+    assert got == tiles
+
+    out = tmp_path / "fused"
+    rc, err = compile_chain(L, src, out, tiles)
+    assert rc == 0, err
+    launch = json.loads((out / "05.out.hip.launch.json").read_text())
+    assert launch["problem"]["m"] == cfg.m and launch["problem"]["n"] == cfg.n
+    assert launch["path"] == path and launch["entry"] == "wtc_matmul_softmax"
+    assert launch["runtime_scales"] == (cfg.in_dtype == "fp8")
+    assert abs(launch["logit_scale"] - cfg.logit_scale) < 1e-6
+    plan_json = json.loads((out / "04.kernel.plan.json").read_text())
+    assert plan_json["kernels"][0]["name"].startswith("chain_tile_kernel")
+    report = dict(l.split("=", 1) for l in (out / "kernel_report.txt").read_text().splitlines()
+                  if "=" in l and " " not in l.split("=", 1)[0])
+    assert int(report["launch_kernel_count"]) == (1 if path == "exchange" else 2)
+    assert int(report["mfma_instruction_count"]) > 0
+    assert int(report["scratch_instruction_count"]) == 0 and int(report["vgpr_spill_count"]) == 0
+    assert int(report["kernels_without_resource_record"]) == 0
+    assert (out / "05.out.gfx950.hsaco").stat().st_size > 0
+    # the canonical chain written in stage 03 is itself a valid input
+    out2 = tmp_path / "again"
+    rc, err = compile_chain(L, out / "03.chain.canonical.mlir", out2, tiles)
+    assert rc == 0, err
+    again = json.loads((out2 / "05.out.hip.launch.json").read_text())
+    assert again.pop("softmax_form") == "decomposed"
+    launch.pop("softmax_form")
+    assert again == launch
+
+
+def test_compile_unfused_baseline(L, tmp_path):
+    src = write_chain(tmp_path, CONFIGS["C2"])
+    rc, err = compile_chain(L, src, tmp_path / "baseline", [128, 128, 64, 2, 32], fused=0)
+    assert rc == 0, err
+    plan_json = json.loads((tmp_path / "baseline" / "04.kernel.plan.json").read_text())
+    assert [k["name"].split("<")[0] for k in plan_json["kernels"]] == [
+        "chain_tile_kernel", "rowmax_kernel", "expsub_kernel", "rowsum_kernel", "rowdiv_kernel"]
+    assert (tmp_path / "baseline" / "05.out.rows.gfx950.hsaco").exists()
+
+
+def test_compile_error_codes(L, tmp_path):
+    src = write_chain(tmp_path, CONFIGS["C2"])
+    assert compile_chain(L, src, tmp_path / "o", [0, 128, 64, 2, 32])[0] == 1
+    err = ctypes.create_string_buffer(64)
+    assert L.welder_compile_typical_chain_to_nvvm(b"", b"x", b"", b"", 128, 128, 64, 2, 32, 1, 1, 0,
+                                                  err, 64) == 1
+    assert err.value
+    rc, msg = compile_chain(L, src, tmp_path / "o", [64, 64, 64, 2, 32])  # no such variant
+    assert rc == 2 and b"no gfx950 kernel variant" in msg
+    bad = tmp_path / "bad.mlir"
+    bad.write_text("module { func.func @main() { return } }")
+    rc, msg = compile_chain(L, bad, tmp_path / "o", [128, 128, 64, 2, 32])
+    assert rc == 2 and msg
+    rc, msg = compile_chain(L, tmp_path / "missing.mlir", tmp_path / "o", [128, 128, 64, 2, 32])
+    assert rc == 2
+
+
+def test_solver_error_codes_and_truncation(L, tmp_path):
+    src = write_chain(tmp_path, CONFIGS["C2"])
+    tiles = [ctypes.c_int64() for _ in range(5)]
+    err = ctypes.create_string_buffer(8)
+    rc = L.welder_solver_solve_typical_chain(b"", b"a", b"b", 1, 0, *[ctypes.byref(t) for t in tiles],
+                                             err, 8)
+    assert rc == 1 and len(err.value) == 7  # truncated, NUL-terminated
+    bad = tmp_path / "bad.mlir"
+    bad.write_text("not mlir")
+    assert solve(L, bad, tmp_path)[0] == 2
+    (tmp_path / "plain_file").write_text("x")  # parent directories are created, but not through a file
+    rc, _, msg = solve(L, src, tmp_path / "plain_file" / "dir")
+    assert rc == 4 and msg
+    assert solve(L, src, tmp_path, errsize=0)[0] == 0  # NULL error buffer is allowed
+
+
+@pytest.mark.skipif(not REF_MLIR.exists(), reason="reference chain files not present")
+@pytest.mark.parametrize("fname,expect", [
+    ("matmul_softmax_chain.mlir", None),
+    ("matmul_softmax_chain_f16_native.mlir", (8192, 128, 64, "f16")),
+    ("matmul_softmax_chain_named_softmax.mlir", (8192, 128, 64, "f32")),
+])
+def test_reference_chain_files(L, tmp_path, fname, expect):
+    src = REF_MLIR / fname
+    rc, tiles, err = solve(L, src, tmp_path)
+    assert rc == 0, err
+    rc, err = compile_chain(L, src, tmp_path / "out", tiles)
+    assert rc == 0, err
+    launch = json.loads((tmp_path / "out" / "05.out.hip.launch.json").read_text())
+    if expect:
+        m, n, k, dt = expect
+        assert (launch["problem"]["m"], launch["problem"]["n"], launch["problem"]["k"]) == (m, n, k)
+        assert launch["in_dtype"] == dt

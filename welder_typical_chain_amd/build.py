@@ -2,8 +2,14 @@
 
 - ``libwtc_hip.so``: the gfx950 HIP kernels plus the C-ABI (launcher, and the
   reference's compile / solver entry points), compiled with hipcc.
-- ``wtc-compiler``: the CLI front end (C++17, g++), which dlopens the library
-  exactly as the reference's CLI dlopens its backend libraries.
+- ``libwelder-compile-capi.so`` (a link to ``libwtc_hip.so``) and
+  ``libwelder-solver-capi.so`` (CPU only: chain recogniser + tile solver): the
+  file names the reference's toolchain looks for in its backend build
+  directory (reference compiler/backend/Toolchain.cpp:29-45).
+- ``<source>.gfx950.co``: the device code object of each HIP source, and
+  ``kernel_resources.json``: per kernel, the register / LDS / scratch figures
+  from the code object's metadata and instruction counts (MFMA, LDS DMA,
+  scratch) from its disassembly.  The compile C-ABI reports them.
 
 Everything lands next to this file so the built artefacts travel with the
 source tree.  Run ``python -m welder_typical_chain_amd.build``.
@@ -21,7 +27,14 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 OBJ = PKG / "_build"
 LIB = PKG / "libwtc_hip.so"
-CLI = PKG / "wtc-compiler"
+COMPILE_LIB = PKG / "libwelder-compile-capi.so"
+SOLVER_LIB = PKG / "libwelder-solver-capi.so"
+RESOURCES = PKG / "kernel_resources.json"
+RESOURCES_TSV = PKG / "kernel_resources.tsv"
+TSV_COLUMNS = ["vgpr_count", "agpr_count", "sgpr_count", "vgpr_spill_count", "sgpr_spill_count",
+               "lds_bytes", "scratch_bytes", "mfma", "lds_dma_loads", "ds_read_tr", "scratch_ops",
+               "instructions"]
+LLVM_BIN = Path(os.environ.get("ROCM_PATH", "/opt/rocm")) / "llvm" / "bin"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
@@ -62,19 +75,93 @@ def _compile_one(src: str) -> Path:
     return obj
 
 
+def _code_object(src: str) -> Path:
+    """Device code object of one HIP source (same flags as the library)."""
+    bundle = OBJ / (src + ".bundle")
+    co = PKG / (Path(src).stem + f".{ARCH}.co")
+    _run([HIPCC, *HIP_FLAGS, "--genco", str(CSRC / src), "-o", str(bundle)])
+    _run([str(LLVM_BIN / "clang-offload-bundler"), "--unbundle", "--type=o",
+          f"--targets=hipv4-amdgcn-amd-amdhsa--{ARCH}", f"--input={bundle}", f"--output={co}"])
+    return co
+
+
+def _kernel_resources(code_objects: list[Path]) -> dict:
+    """Per-kernel metadata and instruction counts of our own code objects."""
+    import yaml
+
+    kernels = {}
+    for co in code_objects:
+        notes = subprocess.run([str(LLVM_BIN / "llvm-readelf"), "--notes", str(co)],
+                               capture_output=True, text=True, check=True).stdout
+        start = notes.find("---")
+        end = notes.find("...", start)
+        meta = yaml.safe_load(notes[start:end]) if start >= 0 else {}
+        for k in meta.get("amdhsa.kernels", []):
+            kernels[k[".name"]] = {
+                "code_object": co.name,
+                "vgpr_count": k.get(".vgpr_count"), "agpr_count": k.get(".agpr_count"),
+                "sgpr_count": k.get(".sgpr_count"),
+                "vgpr_spill_count": k.get(".vgpr_spill_count"),
+                "sgpr_spill_count": k.get(".sgpr_spill_count"),
+                "lds_bytes": k.get(".group_segment_fixed_size"),
+                "scratch_bytes": k.get(".private_segment_fixed_size"),
+                "max_flat_workgroup_size": k.get(".max_flat_workgroup_size"),
+            }
+        dis = subprocess.run([str(LLVM_BIN / "llvm-objdump"), "-d", "--no-show-raw-insn", str(co)],
+                             capture_output=True, text=True, check=True).stdout
+        cur = None
+        for line in dis.splitlines():
+            if line.endswith(">:") and "<" in line:
+                cur = kernels.get(line[line.index("<") + 1:-2])
+                if cur is not None:
+                    cur.update(mfma=0, lds_dma_loads=0, ds_read_tr=0, scratch_ops=0, instructions=0)
+                continue
+            if cur is None or not line.startswith("\t"):
+                continue
+            insn = line.split("//")[0].split()
+            if not insn:
+                continue
+            op = insn[0]
+            cur["instructions"] += 1
+            if op.startswith("v_mfma"):
+                cur["mfma"] += 1
+            elif op.startswith("buffer_load") and insn[-1] == "lds":
+                cur["lds_dma_loads"] += 1
+            elif op.startswith("ds_read_b64_tr"):
+                cur["ds_read_tr"] += 1
+            elif op.startswith("scratch_"):
+                cur["scratch_ops"] += 1
+    return {"target": ARCH, "kernels": kernels}
+
+
 def build(verbose: bool = False) -> Path:
     """Compile every source (always; no staleness shortcut) and link."""
+    import json
+
     OBJ.mkdir(exist_ok=True)
     sources = HIP_SOURCES + [s for s in CXX_SOURCES if (CSRC / s).exists()]
-    with cf.ThreadPoolExecutor(max_workers=min(8, len(sources))) as ex:
+    device_only = [s for s in HIP_SOURCES if s != "launch.hip"]
+    with cf.ThreadPoolExecutor(max_workers=8) as ex:
+        co_jobs = [ex.submit(_code_object, s) for s in device_only]
         objs = list(ex.map(_compile_one, sources))
+        code_objects = [j.result() for j in co_jobs]
     tmp = LIB.with_suffix(".so.tmp")
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-o", str(tmp), *map(str, objs)])
     os.replace(tmp, LIB)
-    cli_src = CSRC / "wtc_compiler_main.cpp"
-    if cli_src.exists():
-        _run(["g++", *CXX_FLAGS, "-o", str(CLI), str(cli_src),
-              *[str(o) for o in objs if o.name.endswith(".cpp.o")], "-ldl"])
+    if COMPILE_LIB.is_symlink() or COMPILE_LIB.exists():
+        COMPILE_LIB.unlink()
+    COMPILE_LIB.symlink_to(LIB.name)
+    cpu_objs = [str(OBJ / (s + ".o")) for s in ("chain_recognizer.cpp", "tile_solver.cpp")]
+    tmp = SOLVER_LIB.with_suffix(".so.tmp")
+    _run(["g++", "-shared", "-Wl,--no-undefined", "-o", str(tmp), *cpu_objs])
+    os.replace(tmp, SOLVER_LIB)
+    res = _kernel_resources(code_objects)
+    RESOURCES.write_text(json.dumps(res, indent=1, sort_keys=True) + "\n")
+    # the same figures as a flat table for the compile C-ABI's report
+    rows = ["\t".join(["kernel", "code_object", *TSV_COLUMNS])]
+    for name, k in sorted(res["kernels"].items()):
+        rows.append("\t".join([name, k["code_object"], *(str(k.get(c, 0)) for c in TSV_COLUMNS)]))
+    RESOURCES_TSV.write_text("\n".join(rows) + "\n")
     if verbose:
         print(f"built {LIB}")
     return LIB

@@ -7,8 +7,11 @@
 #include <dlfcn.h>
 
 #include <cstdio>
+#include <cstdlib>
 #include <filesystem>
+#include <map>
 #include <sstream>
+#include <vector>
 
 #include "chain_spec.h"
 #include "wtc/welder_compile_capi.h"
@@ -32,13 +35,47 @@ static const char* path_name(int p) {
   }
 }
 
-// Resource summary of the kernels, from the kernel_resources.json the build
-// writes next to the library (absent: a note says so).
-static std::string resources_for(const std::string& lib) {
+// Per-kernel resources of the library's own code objects, from the
+// kernel_resources.tsv the build writes next to the library: mangled name ->
+// column -> value.
+using ResourceTable = std::map<std::string, std::map<std::string, std::string>>;
+
+static bool load_resources(const std::string& lib, ResourceTable& table, std::string& where) {
+  where = (std::filesystem::path(lib).parent_path() / "kernel_resources.tsv").string();
   std::string text;
-  const std::string p = (std::filesystem::path(lib).parent_path() / "kernel_resources.json").string();
-  if (!read_file(p, text)) return "kernel resources: not recorded (" + p + " missing)\n";
-  return "kernel resources (" + p + "):\n" + text;
+  if (!read_file(where, text)) return false;
+  std::istringstream in(text);
+  std::string line;
+  std::vector<std::string> cols;
+  auto split = [](const std::string& l) {
+    std::vector<std::string> v;
+    std::string cell;
+    std::istringstream ls(l);
+    while (std::getline(ls, cell, '\t')) v.push_back(cell);
+    return v;
+  };
+  if (!std::getline(in, line)) return false;
+  cols = split(line);
+  while (std::getline(in, line)) {
+    const std::vector<std::string> v = split(line);
+    if (v.empty()) continue;
+    auto& row = table[v[0]];
+    for (size_t i = 1; i < v.size() && i < cols.size(); ++i) row[cols[i]] = v[i];
+  }
+  return true;
+}
+
+static const std::map<std::string, std::string>* find_kernel(const ResourceTable& t,
+                                                             const std::string& prefix) {
+  auto it = t.lower_bound(prefix);
+  if (it != t.end() && it->first.compare(0, prefix.size(), prefix) == 0) return &it->second;
+  return nullptr;
+}
+
+static int64_t cell(const std::map<std::string, std::string>* row, const char* col) {
+  if (!row) return 0;
+  auto it = row->find(col);
+  return it == row->end() ? 0 : std::strtoll(it->second.c_str(), nullptr, 10);
 }
 
 static int compile_impl(const char* input_mlir_path, const char* out_dir, int64_t tile_m,
@@ -97,22 +134,31 @@ static int compile_impl(const char* input_mlir_path, const char* out_dir, int64_
   // kernels of the selected path
   struct K {
     std::string name;
+    std::string symbol_prefix;  // of the mangled name in the code object
     int64_t grid;
     int lds;
   };
+  auto chain_sym = [](int in, int out, int epi) {
+    return "_ZN3wtc17chain_tile_kernelILi" + std::to_string(in) + "ELi" + std::to_string(out) +
+           "ELi" + std::to_string(epi) + "E";
+  };
+  const std::string out_t = "ILi" + std::to_string(out_code) + "E";
   std::vector<K> ks;
   const int64_t rows = spec.batch * spec.m;
   if (path == WTC_PATH_EXCHANGE) {
-    ks.push_back({"chain_tile_kernel<" + kin + "," + kout + ",exchange>", grid, 82944});
+    ks.push_back({"chain_tile_kernel<" + kin + "," + kout + ",exchange>",
+                  chain_sym(in_code, out_code, 0), grid, 82944});
   } else if (path == WTC_PATH_SPLIT) {
-    ks.push_back({"chain_tile_kernel<" + kin + "," + kout + ",split>", grid, 0});
-    ks.push_back({"rescale_rows_kernel<" + kout + ">", (rows + 3) / 4, 8192});
+    ks.push_back({"chain_tile_kernel<" + kin + "," + kout + ",split>",
+                  chain_sym(in_code, out_code, 1), grid, 0});
+    ks.push_back({"rescale_rows_kernel<" + kout + ">", "_ZN3wtc19rescale_rows_kernel" + out_t,
+                  (rows + 3) / 4, 8192});
   } else {
-    ks.push_back({"chain_tile_kernel<" + kin + ",f32,logits>", grid, 0});
-    ks.push_back({"rowmax_kernel", rows, 16});
-    ks.push_back({"expsub_kernel", rows, 0});
-    ks.push_back({"rowsum_kernel", rows, 16});
-    ks.push_back({"rowdiv_kernel<" + kout + ">", rows, 0});
+    ks.push_back({"chain_tile_kernel<" + kin + ",f32,logits>", chain_sym(in_code, 0, 2), grid, 0});
+    ks.push_back({"rowmax_kernel", "_ZN3wtc13rowmax_kernel", rows, 16});
+    ks.push_back({"expsub_kernel", "_ZN3wtc13expsub_kernel", rows, 0});
+    ks.push_back({"rowsum_kernel", "_ZN3wtc13rowsum_kernel", rows, 16});
+    ks.push_back({"rowdiv_kernel<" + kout + ">", "_ZN3wtc13rowdiv_kernel" + out_t, rows, 0});
   }
 
   std::ostringstream plan;
@@ -140,18 +186,70 @@ static int compile_impl(const char* input_mlir_path, const char* out_dir, int64_
          << ",\n  \"softmax_form\": \"" << (spec.form == SoftmaxForm::Named ? "named" : "decomposed")
          << "\"\n}\n";
 
+  // Artifact report: the counterpart of the reference's post-bufferize
+  // report (compiler/runtime/PostbufferizeFixups.cpp:60-82), re-targeted to
+  // the gfx950 code object: MFMA instructions instead of nvvm.mma.sync,
+  // scratch instructions / spills instead of PTX ld.local / st.local.
+  ResourceTable table;
+  std::string res_path;
+  const bool have_res = load_resources(lib, table, res_path);
+  int64_t mfma = 0, scratch_ops = 0, scratch_bytes = 0, vspill = 0, sspill = 0, dma = 0, tr = 0;
+  int missing = 0;
+  std::ostringstream per_kernel;
+  for (const K& k : ks) {
+    const auto* row = have_res ? find_kernel(table, k.symbol_prefix) : nullptr;
+    if (!row) ++missing;
+    mfma += cell(row, "mfma");
+    scratch_ops += cell(row, "scratch_ops");
+    scratch_bytes += cell(row, "scratch_bytes");
+    vspill += cell(row, "vgpr_spill_count");
+    sspill += cell(row, "sgpr_spill_count");
+    dma += cell(row, "lds_dma_loads");
+    tr += cell(row, "ds_read_tr");
+    per_kernel << "kernel " << k.name << " grid=" << k.grid << " block=256";
+    if (row)
+      per_kernel << " vgpr=" << cell(row, "vgpr_count") << " agpr=" << cell(row, "agpr_count")
+                 << " sgpr=" << cell(row, "sgpr_count") << " lds_static=" << cell(row, "lds_bytes")
+                 << " lds_dynamic=" << k.lds << " mfma=" << cell(row, "mfma")
+                 << " scratch_bytes=" << cell(row, "scratch_bytes");
+    else
+      per_kernel << " (no resource record)";
+    per_kernel << "\n";
+  }
+  const std::string canonical = emit_canonical_mlir(spec);
   std::ostringstream report;
+  report << "chain_matmul_count=" << (canonical.find("linalg.") != std::string::npos ? 1 : 0) << "\n";
+  report << "launch_kernel_count=" << ks.size() << "\n";
+  report << "mfma_instruction_count=" << mfma << "\n";
+  report << "lds_dma_load_count=" << dma << "\n";
+  report << "lds_transpose_read_count=" << tr << "\n";
+  report << "scratch_instruction_count=" << scratch_ops << "\n";
+  report << "scratch_bytes=" << scratch_bytes << "\n";
+  report << "vgpr_spill_count=" << vspill << "\n";
+  report << "sgpr_spill_count=" << sspill << "\n";
+  report << "kernels_without_resource_record=" << missing << "\n";
+  report << "resources=" << (have_res ? res_path : "missing") << "\n";
   report << "chain: batch=" << spec.batch << " m=" << spec.m << " n=" << spec.n << " k=" << spec.k
          << " in=" << kin << " out=" << kout << " path=" << path_name(path) << "\n";
-  report << "kernels=" << ks.size() << "\n";
-  for (const K& k : ks) report << "  " << k.name << " grid=" << k.grid << " block=256\n";
-  report << resources_for(lib);
+  report << per_kernel.str();
 
-  if (!write_file((od / "03.chain.canonical.mlir").string(), emit_canonical_mlir(spec)) ||
+  if (!write_file((od / "03.chain.canonical.mlir").string(), canonical) ||
       !write_file((od / "04.kernel.plan.json").string(), plan.str()) ||
       !write_file((od / "05.out.hip.launch.json").string(), launch.str()) ||
       !write_file((od / "kernel_report.txt").string(), report.str()))
     return session_fail(std::string("failed to write artefacts into ") + out_dir);
+  // The device code objects holding the path's kernels, when the build left
+  // them next to the library.
+  const std::filesystem::path libdir = std::filesystem::path(lib).parent_path();
+  std::vector<std::pair<std::string, std::string>> cos = {
+      {"fused_matmul_softmax.gfx950.co", "05.out.gfx950.hsaco"}};
+  if (path == WTC_PATH_UNFUSED) cos.push_back({"unfused_chain.gfx950.co", "05.out.rows.gfx950.hsaco"});
+  for (const auto& c : cos) {
+    if (!std::filesystem::exists(libdir / c.first)) continue;
+    std::filesystem::copy_file(libdir / c.first, od / c.second,
+                               std::filesystem::copy_options::overwrite_existing, ec);
+    if (ec) return session_fail("failed to copy the code object into " + std::string(out_dir));
+  }
   if (verbose)
     std::fprintf(stderr, "[wtc-compile] %s -> %s (%s, %zu kernel(s))\n", input_mlir_path, out_dir,
                  path_name(path), ks.size());
