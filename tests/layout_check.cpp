@@ -255,25 +255,24 @@ int main() {
   run(1, "fp8");
   run(4, "f32");
   // tile_of_block: every (row block, column tile) exactly once
-  for (auto rc : std::vector<std::pair<int64_t, int64_t>>{{16, 16}, {8, 256}, {1024, 16}, {2, 3}, {5, 7}, {3, 1}}) {
-    const int64_t R = rc.first, C = rc.second, G = R * C;
-    std::set<std::pair<int64_t, int64_t>> seen2;
-    for (int64_t b = 0; b < G; ++b) {
-      int64_t r, c;
+  for (auto rc : std::vector<std::pair<uint32_t, uint32_t>>{{16, 16}, {8, 256}, {1024, 16}, {2, 3}, {5, 7}, {3, 1}}) {
+    const uint32_t R = rc.first, C = rc.second, G = R * C;
+    std::set<std::pair<uint32_t, uint32_t>> seen2;
+    for (uint32_t b = 0; b < G; ++b) {
+      uint32_t r, c;
       tile_of_block(b, G, R, C, &r, &c);
-      CHECK(r >= 0 && r < R && c >= 0 && c < C, "tile_of_block out of range\n");
+      CHECK(r < R && c < C, "tile_of_block out of range\n");
       seen2.insert({r, c});
     }
-    CHECK((int64_t)seen2.size() == G, "tile_of_block not a bijection for %lldx%lld\n", (long long)R, (long long)C);
+    CHECK(seen2.size() == G, "tile_of_block not a bijection for %ux%u\n", R, C);
   }
-  for (int64_t G : {256LL, 16384LL, 8LL, 100LL, 7LL, 2048LL}) {
-    std::set<int64_t> s;
-    for (int64_t b = 0; b < G; ++b) s.insert(xcd_remap(b, G));
-    CHECK((int64_t)s.size() == G && *s.begin() == 0 && *s.rbegin() == G - 1, "xcd_remap not a bijection for %lld\n",
-          (long long)G);
+  for (uint32_t G : {256u, 16384u, 8u, 100u, 7u, 2048u}) {
+    std::set<uint32_t> s;
+    for (uint32_t b = 0; b < G; ++b) s.insert(xcd_remap(b, G));
+    CHECK(s.size() == G && *s.begin() == 0 && *s.rbegin() == G - 1, "xcd_remap not a bijection for %u\n", G);
     if (G % 8 == 0)
-      for (int64_t b = 0; b < G; ++b)
-        CHECK(xcd_remap(b, G) / (G / 8) == b % 8, "xcd_remap: tile of block %lld off its XCD\n", (long long)b);
+      for (uint32_t b = 0; b < G; ++b)
+        CHECK(xcd_remap(b, G) / (G / 8) == b % 8, "xcd_remap: tile of block %u off its XCD\n", b);
   }
   if (g_fail) {
     std::printf("FAILED (%d)\n", g_fail);

@@ -43,6 +43,7 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
@@ -66,9 +67,12 @@ template <> struct OutTraits<DT_F32> { static constexpr int SZ = 4; };
 template <> struct OutTraits<DT_F16> { static constexpr int SZ = 2; };
 template <> struct OutTraits<DT_BF16> { static constexpr int SZ = 2; };
 
+// The epilogue stages the tile in LDS as f32 rows of kStagePitch floats (the
+// 4-float pad spreads the 32 rows one wave writes at a time over all banks).
+constexpr int kStagePitch = BN + 4;
+
 template <int IN_DT, int OUT_DT> struct EpiLayout {
-  static constexpr int PITCH = BN * OutTraits<OUT_DT>::SZ + 16;  // staging row pitch
-  static constexpr int STAGING = BM * PITCH;
+  static constexpr int STAGING = BM * kStagePitch * 4;
   static constexpr int RING = Ring<IN_DT>::kBytes;
   static constexpr int UNION = STAGING > RING ? STAGING : RING;
   static constexpr int RED_OFF = (UNION + 255) / 256 * 256;
@@ -175,11 +179,17 @@ __device__ inline i32x4 raw_rsrc(const void* base, uint32_t bytes) {
   return r;
 }
 
-// 16 bytes per lane into LDS at lds_base + 16*lane.
+// 16 bytes per lane into LDS at lds_base + 16*lane.  The descriptor and the
+// LDS base are wave-uniform; readfirstlane states that to the compiler so
+// the "s" operands always get scalar registers (free when they already are).
 __device__ inline void dma16(i32x4 rsrc, uint32_t voff, uint32_t lds_base) {
+  i32x4 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r[i] = __builtin_amdgcn_readfirstlane(rsrc[i]);
+  const uint32_t m = __builtin_amdgcn_readfirstlane(lds_base);
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
                :
-               : "s"(lds_base), "v"(voff), "s"(rsrc)
+               : "s"(m), "v"(voff), "s"(r)
                : "memory", "m0");
 }
 
@@ -190,27 +200,68 @@ __device__ inline void wait_loads_barrier() {
   asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "n"(N) : "memory");
 }
 
-struct DmaTile {
+// Per-lane byte offsets of one wave's direct-to-LDS loads, computed once:
+// k-tile kt of A block j is at a_base[j] + kt*128 (masked to the zero range
+// when its chunk lies past K), of B block j at b_base[j] + kt*b_step.  Rows
+// past M and k-rows past K fall outside the descriptors' ranges by
+// themselves; columns past N are parked at kOutOfRange, which stays out of
+// range for every k-tile (kt*b_step < 2^31).
+struct DmaPlan {
   i32x4 ra, rb;
-  int64_t row0, n0, M, N, K, lda, ldb;
-};
+  uint32_t a_base[4], b_base[4];
+  uint32_t a_chunk[4];  // byte offset of the lane's A chunk inside a k-tile
+  uint32_t k_bytes;     // K * 2
+  uint32_t b_step;      // 64 * ldb: bytes of B per k-tile
+  uint32_t lds_a[4], lds_b[4];  // LDS byte offsets of the wave's blocks in a stage
 
-// One k-tile (A and B, 2 x 16 KiB) into the stage at LDS byte address `stage`.
-// wave_u is the wave index as a scalar.
-__device__ inline void dma_tile16(const DmaTile& d, uint32_t stage, int wave_u, int lane, int kt) {
+  // All extents and pitches fit in 31 bits (the launcher checks that one
+  // batch slice of A and of B is below 2 GiB), so everything here is 32-bit.
+  __device__ inline void init(const void* a, const void* b, uint32_t a_bytes, uint32_t b_bytes,
+                              uint32_t row0, uint32_t n0, uint32_t M, uint32_t N, uint32_t K,
+                              uint32_t lda, uint32_t ldb, int wave_u, int lane) {
+    const i32x4 ra_v = raw_rsrc(a, a_bytes), rb_v = raw_rsrc(b, b_bytes);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int b = dma_block(wave_u, j);
-    const int64_t row = d.row0 + dma_a_row(b, lane);
-    const int64_t kb = (int64_t)kt * kKTileBytes + dma_a_chunk(b, lane) * kChunkBytes;
-    const bool oka = row < d.M && kb < d.K * 2;
-    dma16(d.ra, oka ? (uint32_t)(row * d.lda + kb) : kOutOfRange, stage + b * 1024);
-    const int64_t k = (int64_t)kt * (kKTileBytes / 2) + dma_b_row(b, lane);
-    const int64_t n = d.n0 + 8 * dma_b_chunk(b, lane);
-    const bool okb = k < d.K && n < d.N;
-    dma16(d.rb, okb ? (uint32_t)(k * d.ldb + n * 2) : kOutOfRange, stage + A_STAGE_BYTES + b * 1024);
+    for (int i = 0; i < 4; ++i) {  // wave-uniform: keep them in scalar registers
+      ra[i] = __builtin_amdgcn_readfirstlane(ra_v[i]);
+      rb[i] = __builtin_amdgcn_readfirstlane(rb_v[i]);
+    }
+    k_bytes = K * 2;
+    b_step = 64 * ldb;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int blk = dma_block(wave_u, j);
+      const uint32_t row = row0 + (uint32_t)dma_a_row(blk, lane);
+      a_chunk[j] = (uint32_t)dma_a_chunk(blk, lane) * kChunkBytes;
+      a_base[j] = row < M ? row * lda + a_chunk[j] : kOutOfRange;
+      const uint32_t n = n0 + 8u * (uint32_t)dma_b_chunk(blk, lane);
+      b_base[j] = n < N ? (uint32_t)dma_b_row(blk, lane) * ldb + n * 2 : kOutOfRange;
+      lds_a[j] = blk * 1024;
+      lds_b[j] = A_STAGE_BYTES + blk * 1024;
+    }
   }
-}
+
+  // Load j (0..7) of k-tile kt: A block j/2 for even j, B block j/2 for odd j.
+  __device__ inline void issue_one(uint32_t stage, int kt, int j) const {
+    const int q = j >> 1;
+    if (j & 1) {
+      dma16(rb, b_base[q] + (uint32_t)kt * b_step, stage + lds_b[q]);
+    } else {
+      const uint32_t ka = (uint32_t)kt * kKTileBytes;
+      dma16(ra, ka + a_chunk[q] < k_bytes ? a_base[q] + ka : kOutOfRange, stage + lds_a[q]);
+    }
+  }
+
+  // One k-tile (A and B, 2 x 16 KiB) into the stage at LDS byte address `stage`.
+  __device__ inline void issue(uint32_t stage, int kt) const {
+    const uint32_t ka = (uint32_t)kt * kKTileBytes;
+    const uint32_t kb = (uint32_t)kt * b_step;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      dma16(ra, ka + a_chunk[j] < k_bytes ? a_base[j] + ka : kOutOfRange, stage + lds_a[j]);
+      dma16(rb, b_base[j] + kb, stage + lds_b[j]);
+    }
+  }
+};
 
 typedef __fp16 h4 __attribute__((__vector_size__(4 * sizeof(__fp16))));
 
@@ -323,43 +374,67 @@ __device__ inline void mma_stage(const uint8_t* stage, int lane, int wm, int wn,
   }
 }
 
-template <int IN_DT>
-__device__ inline void mma_stage_tr(const uint8_t* stage, int lane, int wm, int wn,
-                                    f32x16 (&acc)[2][2]) {
-  constexpr int S = kChunksPerKTile / 2;
-  Frags f[2];
-  read_frags_tr(stage, lane, wm, wn, 0, f[0]);
+// All MFMA operands of one k-tile for one wave: A fragments [step][m-subtile],
+// B fragments [step][n-subtile] (64 VGPRs).
+struct KTileFrags {
+  u32x4 a[4][2], b[4][2];
+};
+
+// LDS read i (0..23) of a k-tile's fragments: for k-step s = i / 6, reads
+// 6s, 6s+1 are the two A fragments (ds_read_b128) and 6s+2 .. 6s+5 the
+// halves of the two B fragments (ds_read_b64_tr_b16).
+__device__ inline void read_frag_piece(const uint8_t* stage, int lane, int wm, int wn, int i,
+                                       KTileFrags& f) {
+  const int s = i / 6, u = i % 6;
+  const int r = frag_row(lane);
+  if (u < 2) {
+    f.a[s][u] = *reinterpret_cast<const u32x4*>(
+        stage + a_lds_offset(wm * 64 + u * 32 + r, frag_chunk(lane, s)));
+  } else {
+    const int nt = (u - 2) >> 1, h = (u - 2) & 1;
+    const u32x2 v = tr_read(stage + A_STAGE_BYTES +
+                            btr_offset(btr_k(s, h, lane), btr_n(wn * 64 + nt * 32, lane)));
+    f.b[s][nt][2 * h] = v[0];
+    f.b[s][nt][2 * h + 1] = v[1];
+  }
+}
+
+__device__ inline void read_ktile_frags(const uint8_t* stage, int lane, int wm, int wn,
+                                        KTileFrags& f) {
 #pragma unroll
-  for (int s = 0; s < S; ++s) {
-    if (s + 1 < S) read_frags_tr(stage, lane, wm, wn, s + 1, f[(s + 1) & 1]);
-    mma_step<IN_DT>(f[s & 1], acc);
+  for (int i = 0; i < 24; ++i) read_frag_piece(stage, lane, wm, wn, i, f);
+}
+
+// MFMA i (0..15) of a k-tile: k-step i / 4, subtile (mt, nt) = ((i/2)%2, i%2).
+template <int IN_DT>
+__device__ inline void mma_piece(const KTileFrags& f, int i, f32x16 (&acc)[2][2]) {
+  const int s = i >> 2, mt = (i >> 1) & 1, nt = i & 1;
+  if constexpr (IN_DT == DT_F16) {
+    acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+        __builtin_bit_cast(f16x8, f.b[s][nt]), __builtin_bit_cast(f16x8, f.a[s][mt]), acc[mt][nt], 0, 0, 0);
+  } else {
+    acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+        __builtin_bit_cast(bf16x8, f.b[s][nt]), __builtin_bit_cast(bf16x8, f.a[s][mt]), acc[mt][nt], 0, 0, 0);
   }
 }
 
 // -------------------------------------------------------------------------
-// Output conversion
+// Output conversion: four f32 -> two 32-bit words of f16 / bf16 (RNE)
 // -------------------------------------------------------------------------
-template <int OUT_DT> __device__ inline void store4(uint8_t* dst, float x0, float x1,
-                                                    float x2, float x3);
-template <> __device__ inline void store4<DT_F32>(uint8_t* dst, float x0, float x1,
-                                                  float x2, float x3) {
-  u32x4 u = {__builtin_bit_cast(uint32_t, x0), __builtin_bit_cast(uint32_t, x1),
-             __builtin_bit_cast(uint32_t, x2), __builtin_bit_cast(uint32_t, x3)};
-  *reinterpret_cast<u32x4*>(dst) = u;
+template <int OUT_DT> __device__ inline void pack4(const f32x4& x, uint32_t* w0, uint32_t* w1);
+template <> __device__ inline void pack4<DT_F16>(const f32x4& x, uint32_t* w0, uint32_t* w1) {
+  const float x0 = x[0], x1 = x[1], x2 = x[2], x3 = x[3];
+  *w0 = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x0) |
+        ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x1) << 16);
+  *w1 = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x2) |
+        ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x3) << 16);
 }
-template <> __device__ inline void store4<DT_F16>(uint8_t* dst, float x0, float x1,
-                                                  float x2, float x3) {
-  const _Float16 h0 = (_Float16)x0, h1 = (_Float16)x1, h2 = (_Float16)x2, h3 = (_Float16)x3;
-  u32x2 u = {(uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16),
-             (uint32_t)__builtin_bit_cast(uint16_t, h2) | ((uint32_t)__builtin_bit_cast(uint16_t, h3) << 16)};
-  *reinterpret_cast<u32x2*>(dst) = u;
-}
-template <> __device__ inline void store4<DT_BF16>(uint8_t* dst, float x0, float x1,
-                                                   float x2, float x3) {
-  const __bf16 h0 = (__bf16)x0, h1 = (__bf16)x1, h2 = (__bf16)x2, h3 = (__bf16)x3;
-  u32x2 u = {(uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16),
-             (uint32_t)__builtin_bit_cast(uint16_t, h2) | ((uint32_t)__builtin_bit_cast(uint16_t, h3) << 16)};
-  *reinterpret_cast<u32x2*>(dst) = u;
+template <> __device__ inline void pack4<DT_BF16>(const f32x4& x, uint32_t* w0, uint32_t* w1) {
+  const float x0 = x[0], x1 = x[1], x2 = x[2], x3 = x[3];
+  *w0 = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x0) |
+        ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x1) << 16);
+  *w1 = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x2) |
+        ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x3) << 16);
 }
 
 __device__ inline float wave_xor32_max(float x) { return fmaxf(x, __shfl_xor(x, 32)); }
@@ -442,10 +517,10 @@ chain_tile_kernel(const ChainParams p) {
   const int wave = t >> 6;
   const int wm = wave >> 1, wn = wave & 1;
 
-  int64_t rbg, nt;  // row block across batches, column tile
-  tile_of_block(blockIdx.x, gridDim.x, (int64_t)gridDim.x / p.nT, p.nT, &rbg, &nt);
-  const int64_t bt = rbg / p.nRB;
-  const int64_t rb = rbg % p.nRB;
+  uint32_t rbg, nt;  // row block across batches, column tile
+  tile_of_block(blockIdx.x, gridDim.x, gridDim.x / (uint32_t)p.nT, (uint32_t)p.nT, &rbg, &nt);
+  const uint32_t bt = rbg / (uint32_t)p.nRB;
+  const uint32_t rb = rbg - bt * (uint32_t)p.nRB;
   const int64_t row0 = rb * BM;
   const int64_t n0 = nt * BN;
 
@@ -462,12 +537,19 @@ chain_tile_kernel(const ChainParams p) {
   tl.ldb = p.ldb_bytes;
   uint8_t* o_base = p.out + bt * p.o_bstride;
   const int nk = (int)((p.K * SZ + kKTileBytes - 1) / kKTileBytes);
+  // The row block's generation word, as it is before this tile arrives (it
+  // cannot move until this tile has arrived).  Read by every lane,
+  // unconditionally, once the first k-tiles are requested: the load then
+  // stays in flight through the main loop.  (Under `if (t == 0)`, or ahead of
+  // the 32-bit multiply-adds of the load setup -- which the compiler emits as
+  // 64-bit multiply-adds with an undefined high addend that may land on the
+  // load's destination register -- the compiler waits for it right there.)
   uint32_t gen0 = 0;
-  if constexpr (EPI == kEpiExchange) {
-    if (t == 0)
+  auto load_gen0 = [&]() {
+    if constexpr (EPI == kEpiExchange)
       gen0 = __hip_atomic_load(p.sync + kSyncWords * rbg + kSyncWords / 2, __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
-  }
+  };
 
   f32x16 acc[2][2];
 #pragma unroll
@@ -479,33 +561,61 @@ chain_tile_kernel(const ChainParams p) {
 
   if constexpr (Ring<IN_DT>::kDma) {
     // ---- main loop, 16-bit: 4-stage ring of direct-to-LDS loads -----------
-    // k-tile j goes to stage j % 4, issued three iterations before use; each
-    // wave issues 8 loads per k-tile, so "k-tile kt landed" is vmcnt <= 16.
-    // Loads past the last k-tile read zeros into stages never read again.
+    // k-tile j goes to stage j % S.  Iteration kt: wait until k-tile kt+1 has
+    // landed (its fragments are read during this iteration) and every wave
+    // is done with stage (kt-1) % S, refill that stage with k-tile kt+S-1,
+    // read k-tile kt+1's fragments into registers and run k-tile kt's MFMAs
+    // from the fragments read one iteration earlier -- the MFMAs never wait
+    // for LDS.  Each wave issues 8 loads per k-tile.  Loads past the last
+    // k-tile read zeros into stages that are never used.
     constexpr int S = Ring<IN_DT>::kStages;
-    DmaTile d;
-    d.ra = raw_rsrc(p.a + bt * p.a_bstride, (uint32_t)p.a_bstride);
-    d.rb = raw_rsrc(p.b + bt * p.b_bstride, (uint32_t)p.b_bstride);
-    d.row0 = row0;
-    d.n0 = n0;
-    d.M = p.M;
-    d.N = p.N;
-    d.K = p.K;
-    d.lda = p.lda_bytes;
-    d.ldb = p.ldb_bytes;
-    const uint32_t lds0 = (uint32_t)(uintptr_t)(WTC_LDS uint8_t*)smem;
     const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+    DmaPlan d;
+    d.init(p.a + bt * p.a_bstride, p.b + bt * p.b_bstride, (uint32_t)p.a_bstride,
+           (uint32_t)p.b_bstride, (uint32_t)row0, (uint32_t)n0, (uint32_t)p.M, (uint32_t)p.N,
+           (uint32_t)p.K, (uint32_t)p.lda_bytes, (uint32_t)p.ldb_bytes, wave_u, lane);
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(WTC_LDS uint8_t*)smem;
+    if (nk == 0) load_gen0();
     if (nk > 0) {
 #pragma unroll
-      for (int q = 0; q < S - 1; ++q) dma_tile16(d, lds0 + q * STAGE_BYTES, wave_u, lane, q);
-      for (int kt = 0; kt < nk; ++kt) {
-        wait_loads_barrier<8 * (S - 2)>();
-        dma_tile16(d, lds0 + ((kt + S - 1) % S) * STAGE_BYTES, wave_u, lane, kt + S - 1);
-        mma_stage_tr<IN_DT>(smem + (kt % S) * STAGE_BYTES, lane, wm, wn, acc);
+      for (int q = 0; q < S - 1; ++q) d.issue(lds0 + q * STAGE_BYTES, q);
+      load_gen0();  // newer than the k-tile loads: only makes the waits below stricter
+      wait_loads_barrier<8 * (S - 2)>();  // k-tile 0 landed
+      KTileFrags f0, f1;
+      read_ktile_frags(smem, lane, wm, wn, f0);
+      // One k-tile step, in 8 groups of (1 load of k-tile kt+S-1, 3 fragment
+      // reads of k-tile kt+1, 2 MFMAs of k-tile kt).  A wave that issues a
+      // direct-to-LDS load stalls until the memory pipeline accepts it; with
+      // the MFMAs spread between the loads, the matrix core keeps working
+      // through those stalls instead of waiting for all 8 loads to go out.
+      // sched_barrier pins the groups (MFMAs touch no memory, so the
+      // compiler would otherwise move them freely, also across s_barrier).
+      auto step = [&](int kt, const KTileFrags& cur, KTileFrags& next) {
+        __builtin_amdgcn_sched_barrier(0);
+        wait_loads_barrier<8 * (S - 3)>();  // k-tile kt+1 landed; stage (kt-1)%S free
+        __builtin_amdgcn_sched_barrier(0);
+        const uint32_t fill = lds0 + ((kt + S - 1) % S) * STAGE_BYTES;
+        const uint8_t* rd = smem + ((kt + 1) % S) * STAGE_BYTES;
+#pragma unroll
+        for (int g = 0; g < 8; ++g) {
+          d.issue_one(fill, kt + S - 1, g);
+#pragma unroll
+          for (int i = 0; i < 3; ++i) read_frag_piece(rd, lane, wm, wn, 3 * g + i, next);
+          mma_piece<IN_DT>(cur, 2 * g, acc);
+          mma_piece<IN_DT>(cur, 2 * g + 1, acc);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      };
+      for (int kt = 0; kt < nk; kt += 2) {
+        step(kt, f0, f1);
+        if (kt + 1 < nk) step(kt + 1, f1, f0);
       }
       wait_loads_barrier<0>();
     }
-  } else if (nk > 0) {
+  } else if (nk == 0) {
+    load_gen0();
+  } else {
+    load_gen0();
     // ---- main loop, fp8 / f32: PF k-tiles in registers, 2-stage LDS ring --
     // k-tile j lives in R[j % PF] and is loaded PF-1 iterations before the
     // iteration that moves it to LDS.  Loads past the last k-tile read zeros
@@ -544,6 +654,7 @@ chain_tile_kernel(const ChainParams p) {
   // Lane owns output rows m_loc(mt) = wm*64 + mt*32 + lane%32 and, for each
   // nt, the 16 columns n_loc = wn*64 + nt*32 + acc_i(lane, v).
   const int jr = acc_j(lane);
+  const int nvalid = p.N - n0 < BN ? (int)(p.N - n0) : BN;  // columns of this tile inside N
   if constexpr (EPI == kEpiLogits) {
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
@@ -552,19 +663,32 @@ chain_tile_kernel(const ChainParams p) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[mt][nt2][v] *= p.lin_scale;
   } else {
+    // y = c2 * acc (log2 domain); columns past N get -inf (ragged last tile only)
+    if (nvalid == BN) {
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int nt2 = 0; nt2 < 2; ++nt2)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) acc[mt][nt2][v] *= p.c2;
+    } else {
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int nt2 = 0; nt2 < 2; ++nt2)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const int n_loc = wn * 64 + nt2 * 32 + acc_i(lane, v);
+            acc[mt][nt2][v] = n_loc < nvalid ? acc[mt][nt2][v] * p.c2 : -INFINITY;
+          }
+    }
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
       float mx = -INFINITY;
 #pragma unroll
       for (int nt2 = 0; nt2 < 2; ++nt2)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int64_t n = n0 + wn * 64 + nt2 * 32 + acc_i(lane, v);
-          float y = acc[mt][nt2][v] * p.c2;
-          y = (n < p.N) ? y : -INFINITY;
-          acc[mt][nt2][v] = y;
-          mx = fmaxf(mx, y);
-        }
+        for (int v = 0; v < 16; ++v) mx = fmaxf(mx, acc[mt][nt2][v]);
       mx = wave_xor32_max(mx);
       if (lane < 32) redmax[wn * BM + wm * 64 + mt * 32 + jr] = mx;
     }
@@ -586,65 +710,18 @@ chain_tile_kernel(const ChainParams p) {
       if (lane < 32) redsum[wn * BM + row] = sm;
     }
     __syncthreads();
-
     // Publish this tile's row statistics.
     if (t < BM) {
       const float tm = fmaxf(redmax[t], redmax[BM + t]);
       const float ts = redsum[t] + redsum[BM + t];
-      store_stat(p.partial + (rbg * BM + t) * p.nT + nt, tm, ts);
-      factor[t] = 1.0f;
-    }
-    if constexpr (EPI == kEpiExchange) {
-      // statistics stores complete before this tile is counted
-      if (t < BM) __builtin_amdgcn_s_waitcnt(0);
-      __syncthreads();
-      if (t == 0) rowblock_barrier(p.sync + kSyncWords * rbg, gen0, p.nT, p.err, p.spin_ticks);
-      __syncthreads();
-      // Every thread fetches its share of the row block's BM x nT statistics
-      // (independent loads, one round trip), parks them in LDS (the ring is
-      // free now), then one thread per row merges its nT pairs.
-      float2* stats = reinterpret_cast<float2*>(smem);
-      const float2* st = p.partial + rbg * BM * p.nT;
-      const int total = BM * p.nT;
-      for (int i0 = 0; i0 < total; i0 += 8 * NTHREADS) {
-        float2 v[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          const int i = i0 + u * NTHREADS + t;
-          v[u] = i < total ? load_stat(st + i) : make_float2(-INFINITY, 0.0f);
-        }
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          const int i = i0 + u * NTHREADS + t;
-          if (i < total) stats[i] = v[u];
-        }
-      }
-      __syncthreads();
-      if (t < BM) {
-        float gm = -INFINITY, gs = 0.0f;
-        for (int q = 0; q < p.nT; ++q) {  // online merge of (max, sum) pairs
-          const float2 s2 = stats[t * p.nT + q];
-          const float nm = fmaxf(gm, s2.x);
-          gs = gs * __builtin_amdgcn_exp2f(gm - nm) + s2.y * __builtin_amdgcn_exp2f(s2.x - nm);
-          gm = nm;
-        }
-        const float tm = fmaxf(redmax[t], redmax[BM + t]);
-        factor[t] = __builtin_amdgcn_exp2f(tm - gm) / gs;
-      }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      const float f = factor[wm * 64 + mt * 32 + jr];
-#pragma unroll
-      for (int nt2 = 0; nt2 < 2; ++nt2)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) acc[mt][nt2][v] *= f;
+      store_stat(p.partial + ((int64_t)rbg * BM + t) * p.nT + nt, tm, ts);
     }
   }
 
-  // ---- stage the tile in LDS, then 128-bit coalesced stores ------------------
-  constexpr int OSZ = OutTraits<OUT_DT>::SZ;
+  // Stage the tile in LDS as f32 (the ring is free: every load has landed
+  // and every wave is past the last k-tile).  For the exchange path this
+  // happens before the row-block wait, so the wait hides it.
+  float* stg = reinterpret_cast<float*>(smem);
 #pragma unroll
   for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
@@ -653,20 +730,71 @@ chain_tile_kernel(const ChainParams p) {
       for (int g = 0; g < 4; ++g) {
         const int m_loc = wm * 64 + mt * 32 + jr;
         const int n_loc = wn * 64 + nt2 * 32 + acc_i(lane, 4 * g);
-        store4<OUT_DT>(smem + m_loc * L::PITCH + n_loc * OSZ, acc[mt][nt2][4 * g],
-                       acc[mt][nt2][4 * g + 1], acc[mt][nt2][4 * g + 2], acc[mt][nt2][4 * g + 3]);
+        *reinterpret_cast<f32x4*>(stg + m_loc * kStagePitch + n_loc) =
+            f32x4{acc[mt][nt2][4 * g], acc[mt][nt2][4 * g + 1], acc[mt][nt2][4 * g + 2],
+                  acc[mt][nt2][4 * g + 3]};
       }
+
+  if constexpr (EPI == kEpiExchange) {
+    // statistics stores complete before this tile is counted
+    if (t < BM) __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (t == 0) rowblock_barrier(p.sync + kSyncWords * rbg, gen0, p.nT, p.err, p.spin_ticks);
+    __syncthreads();
+    // Two threads per row each merge half of the row's nT (max, sum) pairs,
+    // loaded straight from the workspace in batches of 8 independent loads,
+    // then combine with their partner lane.
+    const int r = t >> 1, h = t & 1;
+    const int half = (p.nT + 1) >> 1;
+    const int q0 = h * half, q1 = q0 + half < p.nT ? q0 + half : p.nT;
+    const float2* st = p.partial + ((int64_t)rbg * BM + r) * p.nT;
+    float gm = -INFINITY, gs = 0.0f;
+    for (int qb = q0; qb < q1; qb += 8) {
+      float2 v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        v[u] = qb + u < q1 ? load_stat(st + qb + u) : make_float2(-INFINITY, 0.0f);
+      float cm = v[0].x;
+#pragma unroll
+      for (int u = 1; u < 8; ++u) cm = fmaxf(cm, v[u].x);
+      const float nm = fmaxf(gm, cm);
+      float cs = gs * __builtin_amdgcn_exp2f(gm - nm);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) cs += v[u].y * __builtin_amdgcn_exp2f(v[u].x - nm);
+      gm = nm;
+      gs = cs;
+    }
+    // gm == -inf only for an empty half (nT == 1); its sum is 0
+    const float om = __shfl_xor(gm, 1), os = __shfl_xor(gs, 1);
+    const float M = fmaxf(gm, om);
+    const float S = (gm == -INFINITY ? 0.0f : gs * __builtin_amdgcn_exp2f(gm - M)) +
+                    (om == -INFINITY ? 0.0f : os * __builtin_amdgcn_exp2f(om - M));
+    if (h == 0) factor[r] = __builtin_amdgcn_exp2f(fmaxf(redmax[r], redmax[BM + r]) - M) / S;
+  }
   __syncthreads();
-  constexpr int CPR = BN * OSZ / 16;  // 16-byte chunks per tile row
-  constexpr int EPC = 16 / OSZ;       // elements per chunk
+
+  // ---- scale, convert and store: 16 output bytes per thread per step -------
+  constexpr int OSZ = OutTraits<OUT_DT>::SZ;
+  constexpr int EPC = 16 / OSZ;       // elements per 16-byte chunk
+  constexpr int CPR = BN / EPC;       // chunks per tile row
 #pragma unroll 4
   for (int idx = t; idx < BM * CPR; idx += NTHREADS) {
     const int row = idx / CPR, ch = idx % CPR;
     const int64_t m = row0 + row;
     const int64_t n = n0 + ch * EPC;
     if (m < p.M && n < p.N) {
-      const u32x4 u = *reinterpret_cast<const u32x4*>(smem + row * L::PITCH + ch * 16);
-      *reinterpret_cast<u32x4*>(o_base + m * p.ldo_bytes + n * OSZ) = u;
+      const float f = EPI == kEpiExchange ? factor[row] : 1.0f;
+      const float* src = stg + row * kStagePitch + ch * EPC;
+      const f32x4 x0 = *reinterpret_cast<const f32x4*>(src) * f;
+      if constexpr (OSZ == 4) {
+        *reinterpret_cast<f32x4*>(o_base + m * p.ldo_bytes + n * OSZ) = x0;
+      } else {
+        const f32x4 x1 = *reinterpret_cast<const f32x4*>(src + 4) * f;
+        uint32_t w0, w1, w2, w3;
+        pack4<OUT_DT>(x0, &w0, &w1);
+        pack4<OUT_DT>(x1, &w2, &w3);
+        *reinterpret_cast<u32x4*>(o_base + m * p.ldo_bytes + n * OSZ) = u32x4{w0, w1, w2, w3};
+      }
     }
   }
 }

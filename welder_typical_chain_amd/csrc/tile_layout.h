@@ -153,19 +153,20 @@ WTC_HD constexpr int btr_n(int nb, int lane) { return nb + 16 * ((lane >> 4) & 1
 // fetch over the fabric.
 constexpr int kGroupRows = 4;
 
-WTC_HD constexpr int64_t xcd_remap(int64_t b, int64_t G) {
+WTC_HD constexpr uint32_t xcd_remap(uint32_t b, uint32_t G) {
   return (G % 8 == 0) ? (b % 8) * (G / 8) + b / 8 : b;
 }
 
 // rows = row blocks (over all batches), cols = column tiles per row block.
-WTC_HD void tile_of_block(int64_t b, int64_t G, int64_t rows, int64_t cols,
-                                 int64_t* row, int64_t* col) {
-  const int64_t t = xcd_remap(b, G);
-  const int64_t per_group = (int64_t)kGroupRows * cols;
-  const int64_t group = t / per_group;
-  const int64_t first = group * kGroupRows;
-  const int64_t in_group = (rows - first) < kGroupRows ? (rows - first) : kGroupRows;
-  const int64_t r = t - group * per_group;
+// 32-bit arithmetic: the launcher keeps grids below 2^31 workgroups.
+WTC_HD void tile_of_block(uint32_t b, uint32_t G, uint32_t rows, uint32_t cols, uint32_t* row,
+                          uint32_t* col) {
+  const uint32_t t = xcd_remap(b, G);
+  const uint32_t per_group = (uint32_t)kGroupRows * cols;
+  const uint32_t group = t / per_group;
+  const uint32_t first = group * kGroupRows;
+  const uint32_t in_group = (rows - first) < (uint32_t)kGroupRows ? (rows - first) : kGroupRows;
+  const uint32_t r = t - group * per_group;
   *row = first + r % in_group;
   *col = r / in_group;
 }
