@@ -19,7 +19,6 @@ from __future__ import annotations
 
 import argparse
 import json
-import math
 import os
 import sys
 import time
@@ -40,6 +39,9 @@ def parse():
     ap.add_argument("--path", default="auto", choices=["auto", "exchange", "split", "unfused"])
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="budget of the cpu_baseline sample (0 disables it)")
+    ap.add_argument("--workload", default="C2", choices=["C2", "C3", "C4", "C5"],
+                    help="C2 is the headline; C3-C5 are the other BASELINE.json configurations, "
+                         "timed the same way (no cpu_baseline, no committed traffic figure)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="before the timed steps, run plain device copies of this many MiB "
                          "(the byte-count calibration for rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -61,6 +63,36 @@ def cpu_baseline(a_host, b_host, n, k, budget_s):
                       f"OpenMP over rows), {secs:.1f} s"}
 
 
+PEAKS = {"f16": PEAK_F16_TFLOPS, "bf16": PEAK_F16_TFLOPS, "fp8": 5000.0}
+TORCH_DT = {"f16": "float16", "bf16": "bfloat16", "fp8": "float8_e4m3fn", "f32": "float32"}
+
+
+def make_workload(cfg, dev, torch):
+    """Synthetic inputs of the configuration's distribution, generated on the GPU.
+    Returns (a, b, logit_scale, scale_a, scale_b)."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    bshape = (cfg.batch,) if cfg.batch > 1 else ()
+    sa = (*bshape, cfg.m, cfg.k)
+    sb = (*bshape, cfg.k, cfg.n)
+    if cfg.dist == "uniform":
+        a32 = (torch.rand(sa, generator=g, device=dev) * 2 - 1) * cfg.dist_param
+        b32 = (torch.rand(sb, generator=g, device=dev) * 2 - 1) * cfg.dist_param
+    else:
+        a32 = torch.randn(sa, generator=g, device=dev) * cfg.dist_param
+        b32 = torch.randn(sb, generator=g, device=dev) * cfg.dist_param
+    if cfg.in_dtype == "fp8":  # per-tensor amax scaling onto e4m3's range
+        scale_a = float(a32.abs().max()) / 448.0
+        scale_b = float(b32.abs().max()) / 448.0
+        a = (a32 / scale_a).to(torch.float8_e4m3fn)
+        b = (b32 / scale_b).to(torch.float8_e4m3fn)
+    else:
+        scale_a = scale_b = 1.0
+        a = a32.to(getattr(torch, TORCH_DT[cfg.in_dtype]))
+        b = b32.to(getattr(torch, TORCH_DT[cfg.in_dtype]))
+    return a.contiguous(), b.contiguous(), cfg.logit_scale, scale_a, scale_b
+
+
 def load_traffic():
     p = ROOT / "profiles" / "c2_f16_exchange_traffic.json"
     if not p.exists():
@@ -80,23 +112,27 @@ def main():
     import torch
     from welder_typical_chain_amd import _lib
     from welder_typical_chain_amd.chain import matmul_softmax, new_workspace, workspace_size
-    from welder_typical_chain_amd.configs import HEADLINE as cfg
+    from welder_typical_chain_amd.configs import CONFIGS
 
+    cfg = CONFIGS[args.workload]
+    headline = args.workload == "C2"
     if not _lib.LIB_PATH.exists():
         from welder_typical_chain_amd import build
         build.build()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     m, n, k = cfg.m, cfg.n, cfg.k
-    g = torch.Generator(device=dev)
-    g.manual_seed(0)
-    a = (torch.randn((m, k), generator=g, device=dev) / math.sqrt(k)).to(torch.float16)
-    b = (torch.randn((k, n), generator=g, device=dev) / math.sqrt(k)).to(torch.float16)
-    out = torch.empty((m, n), dtype=torch.float16, device=dev)
-    ws = new_workspace(workspace_size(1, m, n, k, _lib.DTYPE_F16, _lib.DTYPE_F16, args.path), dev)
+    a, b, logit_scale, scale_a, scale_b = make_workload(cfg, dev, torch)
+    out_dt = getattr(torch, TORCH_DT[cfg.out_dtype])
+    out = torch.empty((*a.shape[:-2], m, n), dtype=out_dt, device=dev)
+    in_code = {"f32": _lib.DTYPE_F32, "f16": _lib.DTYPE_F16, "bf16": _lib.DTYPE_BF16,
+               "fp8": _lib.DTYPE_FP8_E4M3}[cfg.in_dtype]
+    out_code = {"f32": _lib.DTYPE_F32, "f16": _lib.DTYPE_F16, "bf16": _lib.DTYPE_BF16}[cfg.out_dtype]
+    ws = new_workspace(workspace_size(cfg.batch, m, n, k, in_code, out_code, args.path), dev)
 
     def step():
-        matmul_softmax(a, b, out=out, path=args.path, workspace=ws)
+        matmul_softmax(a, b, out=out, path=args.path, workspace=ws, logit_scale=logit_scale,
+                       scale_a=scale_a, scale_b=scale_b)
 
     if args.copy_probe_mib > 0:
         n_el = args.copy_probe_mib * (1 << 20) // 4
@@ -125,11 +161,37 @@ def main():
     tflops = flops / (ms * 1e-3) / 1e12
     from welder_typical_chain_amd.chain import read_error_flags
     flags = read_error_flags(ws)
-    row_dev = float((out.float().sum(-1) - 1).abs().max())
+    row_dev = float((out.float().sum(-1) - 1).abs().max()) if out.numel() <= (1 << 28) else \
+        float((out[..., :256, :].float().sum(-1) - 1).abs().max())
 
     cpu = None
-    if args.cpu_seconds > 0:
+    if args.cpu_seconds > 0 and headline:
         cpu = cpu_baseline(a.float().cpu().numpy(), b.float().cpu().numpy(), n, k, args.cpu_seconds)
+
+    peak = PEAKS[cfg.in_dtype]
+    alg_bytes = (a.numel() * a.element_size() + b.numel() * b.element_size() +
+                 out.numel() * out.element_size())
+    gbs = alg_bytes / (ms * 1e-3) / 1e9
+    if not headline:
+        # HBM-bound when the arithmetic intensity is under the ridge point
+        mfma_bound = flops / alg_bytes > peak * 1e12 / (PEAK_HBM_GBS * 1e9)
+        line = {
+            "metric": f"fused matmul+softmax TFLOP/s ({cfg.name})",
+            "value": round(tflops, 3), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": ms, "us_per_call": ms * 1e3,
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": cfg.in_dtype, "data": f"synthetic {cfg.dist} inputs generated on the GPU",
+            "config": {"workload": cfg.name, "batch": cfg.batch, "m": m, "n": n, "k": k,
+                       "in_dtype": cfg.in_dtype, "out_dtype": cfg.out_dtype, "path": args.path},
+            "roofline": ({"bound": "mfma", "achieved": round(tflops, 3), "peak": peak,
+                          "unit": "TFLOP/s", "frac": round(tflops / peak, 4), "traffic": None}
+                         if mfma_bound else
+                         {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
+                          "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None}),
+            "checks": {"row_sum_max_dev": row_dev, "device_error_flags": flags},
+        }
+        print(json.dumps(line), flush=True)
+        return
 
     line = {
         "metric": "fused matmul+softmax TFLOP/s & % f16 MFMA peak (M=N=2048,K=1024)",

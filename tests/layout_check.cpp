@@ -196,9 +196,9 @@ static void run_dma16() {
     for (int n = 0; n < BN; ++n) B[k * BN + n] = (uint16_t)((k * 5 + n * 11) % 17 + 1);
   std::vector<uint8_t> sa(BM * 128), sb(KE * 256);
   std::vector<int> ca(sa.size(), 0), cb(sb.size(), 0);
-  for (int w = 0; w < 4; ++w)
-    for (int j = 0; j < 4; ++j) {
-      const int b = dma_block(w, j);
+  for (int w = 0; w < 8; ++w)  // the 8-wave layout: 2 blocks per wave and operand
+    for (int j = 0; j < 2; ++j) {
+      const int b = dma_block(w, j, 2);
       for (int i = 0; i < 64; ++i) {
         const int row = dma_a_row(b, i), c = dma_a_chunk(b, i);
         const int dst = b * 1024 + 16 * i;
@@ -213,11 +213,11 @@ static void run_dma16() {
     }
   for (size_t i = 0; i < ca.size(); ++i) CHECK(ca[i] == 1 && cb[i] == 1, "[dma16] LDS byte %zu coverage\n", i);
   Conflicts cr;
-  for (int wave = 0; wave < 4; ++wave) {
-    const int wn = wave & 1;
+  for (int wave = 0; wave < 8; ++wave) {  // 2 x 4 waves, 32 columns each
+    const int wn = wave & 3;
     for (int s = 0; s < 4; ++s)
-      for (int nt = 0; nt < 2; ++nt) {
-        const int nb = wn * 64 + nt * 32;
+      for (int nt = 0; nt < 1; ++nt) {
+        const int nb = wn * 32 + nt * 32;
         uint16_t op[64][8];
         for (int h = 0; h < 2; ++h) {
           uint16_t src[64][4];

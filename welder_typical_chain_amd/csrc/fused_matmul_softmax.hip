@@ -49,17 +49,23 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int BM = 128;
 constexpr int BN = 128;
-constexpr int NTHREADS = 256;
 constexpr int A_STAGE_BYTES = BM * kKTileBytes;                  // 16 KiB
 constexpr int STAGE_BYTES = A_STAGE_BYTES + BN * kKTileBytes;    // 32 KiB
 constexpr uint32_t kOutOfRange = 0x80000000u;  // buffer offset that reads 0
 
-// 16-bit inputs stream through a 4-stage ring filled by direct-to-LDS loads;
-// fp8 / f32 through a 2-stage ring filled from registers.
-template <int IN_DT> struct Ring {
+// Per input type: 16-bit inputs stream through a 4-stage ring filled by
+// direct-to-LDS loads and run 8 waves (2 per SIMD: while one waits to issue
+// a load, the other issues MFMAs), each owning a 64x32 block; fp8 / f32 go
+// through a 2-stage ring filled from registers with 4 waves of 64x64.
+template <int IN_DT> struct Cfg {
   static constexpr bool kDma = IN_DT == DT_F16 || IN_DT == DT_BF16;
+  static constexpr int kWavesN = kDma ? 4 : 2;          // waves along N (2 along M)
+  static constexpr int kWaves = 2 * kWavesN;
+  static constexpr int kThreads = 64 * kWaves;
+  static constexpr int kNT = BN / kWavesN / 32;          // 32-column subtiles per wave
+  static constexpr int kBlocksPerWave = 16 / kWaves;     // 1 KiB load blocks per operand
   static constexpr int kStages = kDma ? 4 : 2;
-  static constexpr int kBytes = kStages * STAGE_BYTES;
+  static constexpr int kRingBytes = kStages * STAGE_BYTES;
 };
 
 template <int OUT_DT> struct OutTraits;
@@ -73,11 +79,11 @@ constexpr int kStagePitch = BN + 4;
 
 template <int IN_DT, int OUT_DT> struct EpiLayout {
   static constexpr int STAGING = BM * kStagePitch * 4;
-  static constexpr int RING = Ring<IN_DT>::kBytes;
+  static constexpr int RING = Cfg<IN_DT>::kRingBytes;
   static constexpr int UNION = STAGING > RING ? STAGING : RING;
   static constexpr int RED_OFF = (UNION + 255) / 256 * 256;
-  // redmax[2][BM], redsum[2][BM], factor[BM]  (floats)
-  static constexpr int TOTAL = RED_OFF + 5 * BM * 4;
+  // redmax[kWavesN][BM], redsum[kWavesN][BM], factor[BM]  (floats)
+  static constexpr int TOTAL = RED_OFF + (2 * Cfg<IN_DT>::kWavesN + 1) * BM * 4;
 };
 
 __device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
@@ -206,13 +212,14 @@ __device__ inline void wait_loads_barrier() {
 // past M and k-rows past K fall outside the descriptors' ranges by
 // themselves; columns past N are parked at kOutOfRange, which stays out of
 // range for every k-tile (kt*b_step < 2^31).
+template <int NB>  // 1 KiB blocks per operand per wave
 struct DmaPlan {
   i32x4 ra, rb;
-  uint32_t a_base[4], b_base[4];
-  uint32_t a_chunk[4];  // byte offset of the lane's A chunk inside a k-tile
-  uint32_t k_bytes;     // K * 2
-  uint32_t b_step;      // 64 * ldb: bytes of B per k-tile
-  uint32_t lds_a[4], lds_b[4];  // LDS byte offsets of the wave's blocks in a stage
+  uint32_t a_base[NB], b_base[NB];
+  uint32_t a_chunk[NB];  // byte offset of the lane's A chunk inside a k-tile
+  uint32_t k_bytes;      // K * 2
+  uint32_t b_step;       // 64 * ldb: bytes of B per k-tile
+  uint32_t lds_a[NB], lds_b[NB];  // LDS byte offsets of the wave's blocks in a stage
 
   // All extents and pitches fit in 31 bits (the launcher checks that one
   // batch slice of A and of B is below 2 GiB), so everything here is 32-bit.
@@ -228,8 +235,8 @@ struct DmaPlan {
     k_bytes = K * 2;
     b_step = 64 * ldb;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int blk = dma_block(wave_u, j);
+    for (int j = 0; j < NB; ++j) {
+      const int blk = dma_block(wave_u, j, NB);
       const uint32_t row = row0 + (uint32_t)dma_a_row(blk, lane);
       a_chunk[j] = (uint32_t)dma_a_chunk(blk, lane) * kChunkBytes;
       a_base[j] = row < M ? row * lda + a_chunk[j] : kOutOfRange;
@@ -240,7 +247,7 @@ struct DmaPlan {
     }
   }
 
-  // Load j (0..7) of k-tile kt: A block j/2 for even j, B block j/2 for odd j.
+  // Load j (0 .. 2*NB-1) of k-tile kt: A block j/2 for even j, B block j/2 for odd j.
   __device__ inline void issue_one(uint32_t stage, int kt, int j) const {
     const int q = j >> 1;
     if (j & 1) {
@@ -251,15 +258,11 @@ struct DmaPlan {
     }
   }
 
-  // One k-tile (A and B, 2 x 16 KiB) into the stage at LDS byte address `stage`.
+  // One k-tile (A and B, 2 x 16 KiB over all waves) into the stage at LDS
+  // byte address `stage`.
   __device__ inline void issue(uint32_t stage, int kt) const {
-    const uint32_t ka = (uint32_t)kt * kKTileBytes;
-    const uint32_t kb = (uint32_t)kt * b_step;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      dma16(ra, ka + a_chunk[j] < k_bytes ? a_base[j] + ka : kOutOfRange, stage + lds_a[j]);
-      dma16(rb, b_base[j] + kb, stage + lds_b[j]);
-    }
+    for (int j = 0; j < 2 * NB; ++j) issue_one(stage, kt, j);
   }
 };
 
@@ -375,17 +378,20 @@ __device__ inline void mma_stage(const uint8_t* stage, int lane, int wm, int wn,
 }
 
 // All MFMA operands of one k-tile for one wave: A fragments [step][m-subtile],
-// B fragments [step][n-subtile] (64 VGPRs).
+// B fragments [step][n-subtile].
+template <int NTN>
 struct KTileFrags {
-  u32x4 a[4][2], b[4][2];
+  u32x4 a[4][2], b[4][NTN];
 };
 
-// LDS read i (0..23) of a k-tile's fragments: for k-step s = i / 6, reads
-// 6s, 6s+1 are the two A fragments (ds_read_b128) and 6s+2 .. 6s+5 the
-// halves of the two B fragments (ds_read_b64_tr_b16).
-__device__ inline void read_frag_piece(const uint8_t* stage, int lane, int wm, int wn, int i,
-                                       KTileFrags& f) {
-  const int s = i / 6, u = i % 6;
+// LDS read i of a k-tile's fragments (2 + 2*NTN reads per k-step s): the two
+// A fragments (ds_read_b128), then the halves of the NTN B fragments
+// (ds_read_b64_tr_b16).  The wave's B columns start at nw.
+template <int NTN>
+__device__ inline void read_frag_piece(const uint8_t* stage, int lane, int wm, int nw, int i,
+                                       KTileFrags<NTN>& f) {
+  constexpr int RPS = 2 + 2 * NTN;
+  const int s = i / RPS, u = i % RPS;
   const int r = frag_row(lane);
   if (u < 2) {
     f.a[s][u] = *reinterpret_cast<const u32x4*>(
@@ -393,22 +399,17 @@ __device__ inline void read_frag_piece(const uint8_t* stage, int lane, int wm, i
   } else {
     const int nt = (u - 2) >> 1, h = (u - 2) & 1;
     const u32x2 v = tr_read(stage + A_STAGE_BYTES +
-                            btr_offset(btr_k(s, h, lane), btr_n(wn * 64 + nt * 32, lane)));
+                            btr_offset(btr_k(s, h, lane), btr_n(nw + nt * 32, lane)));
     f.b[s][nt][2 * h] = v[0];
     f.b[s][nt][2 * h + 1] = v[1];
   }
 }
 
-__device__ inline void read_ktile_frags(const uint8_t* stage, int lane, int wm, int wn,
-                                        KTileFrags& f) {
-#pragma unroll
-  for (int i = 0; i < 24; ++i) read_frag_piece(stage, lane, wm, wn, i, f);
-}
-
-// MFMA i (0..15) of a k-tile: k-step i / 4, subtile (mt, nt) = ((i/2)%2, i%2).
-template <int IN_DT>
-__device__ inline void mma_piece(const KTileFrags& f, int i, f32x16 (&acc)[2][2]) {
-  const int s = i >> 2, mt = (i >> 1) & 1, nt = i & 1;
+// MFMA i of a k-tile (2*NTN per k-step): k-step i / (2*NTN), subtile
+// (mt, nt) = ((i / NTN) % 2, i % NTN).
+template <int IN_DT, int NTN>
+__device__ inline void mma_piece(const KTileFrags<NTN>& f, int i, f32x16 (&acc)[2][NTN]) {
+  const int s = i / (2 * NTN), mt = (i / NTN) & 1, nt = i % NTN;
   if constexpr (IN_DT == DT_F16) {
     acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
         __builtin_bit_cast(f16x8, f.b[s][nt]), __builtin_bit_cast(f16x8, f.a[s][mt]), acc[mt][nt], 0, 0, 0);
@@ -504,18 +505,23 @@ __device__ inline void rowblock_barrier(uint32_t* cnt_gen, uint32_t g0, int nT, 
 // The kernel
 // -------------------------------------------------------------------------
 template <int IN_DT, int OUT_DT, int EPI, int PF>
-__global__ void __launch_bounds__(NTHREADS, 1)
+__global__ void __launch_bounds__(Cfg<IN_DT>::kThreads, 1)
 chain_tile_kernel(const ChainParams p) {
+  using C = Cfg<IN_DT>;
   using L = EpiLayout<IN_DT, OUT_DT>;
+  constexpr int NT = C::kThreads;
+  constexpr int WN = C::kWavesN;
+  constexpr int NTN = C::kNT;
   __shared__ __attribute__((aligned(16))) uint8_t smem[L::TOTAL];
-  float* redmax = reinterpret_cast<float*>(smem + L::RED_OFF);
-  float* redsum = redmax + 2 * BM;
-  float* factor = redsum + 2 * BM;
+  float* redmax = reinterpret_cast<float*>(smem + L::RED_OFF);  // [WN][BM]
+  float* redsum = redmax + WN * BM;                              // [WN][BM]
+  float* factor = redsum + WN * BM;                              // [BM]
 
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int wave = t >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WN, wn = wave % WN;
+  const int nw = wn * 32 * NTN;  // first column of the wave's block
 
   uint32_t rbg, nt;  // row block across batches, column tile
   tile_of_block(blockIdx.x, gridDim.x, gridDim.x / (uint32_t)p.nT, (uint32_t)p.nT, &rbg, &nt);
@@ -525,16 +531,6 @@ chain_tile_kernel(const ChainParams p) {
   const int64_t n0 = nt * BN;
 
   constexpr int SZ = dtype_bytes(IN_DT);
-  Tile tl;
-  tl.ra = make_rsrc(p.a + bt * p.a_bstride, (uint32_t)p.a_bstride);
-  tl.rb = make_rsrc(p.b + bt * p.b_bstride, (uint32_t)p.b_bstride);
-  tl.row0 = row0;
-  tl.n0 = n0;
-  tl.M = p.M;
-  tl.N = p.N;
-  tl.K = p.K;
-  tl.lda = p.lda_bytes;
-  tl.ldb = p.ldb_bytes;
   uint8_t* o_base = p.out + bt * p.o_bstride;
   const int nk = (int)((p.K * SZ + kKTileBytes - 1) / kKTileBytes);
   // The row block's generation word, as it is before this tile arrives (it
@@ -551,26 +547,31 @@ chain_tile_kernel(const ChainParams p) {
                                __HIP_MEMORY_SCOPE_AGENT);
   };
 
-  f32x16 acc[2][2];
+  f32x16 acc[2][NTN];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < NTN; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-  if constexpr (Ring<IN_DT>::kDma) {
+  if constexpr (C::kDma) {
     // ---- main loop, 16-bit: 4-stage ring of direct-to-LDS loads -----------
     // k-tile j goes to stage j % S.  Iteration kt: wait until k-tile kt+1 has
     // landed (its fragments are read during this iteration) and every wave
     // is done with stage (kt-1) % S, refill that stage with k-tile kt+S-1,
     // read k-tile kt+1's fragments into registers and run k-tile kt's MFMAs
     // from the fragments read one iteration earlier -- the MFMAs never wait
-    // for LDS.  Each wave issues 8 loads per k-tile.  Loads past the last
+    // for LDS.  Each wave issues LPT loads per k-tile.  Loads past the last
     // k-tile read zeros into stages that are never used.
-    constexpr int S = Ring<IN_DT>::kStages;
+    constexpr int S = C::kStages;
+    constexpr int NB = C::kBlocksPerWave;
+    constexpr int LPT = 2 * NB;            // loads per wave per k-tile
+    constexpr int RPT = 4 * (2 + 2 * NTN);  // fragment reads per wave per k-tile
+    constexpr int MPT = 4 * 2 * NTN;        // MFMAs per wave per k-tile
+    static_assert(RPT % LPT == 0 && MPT % LPT == 0, "k-tile step groups");
     const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-    DmaPlan d;
+    DmaPlan<NB> d;
     d.init(p.a + bt * p.a_bstride, p.b + bt * p.b_bstride, (uint32_t)p.a_bstride,
            (uint32_t)p.b_bstride, (uint32_t)row0, (uint32_t)n0, (uint32_t)p.M, (uint32_t)p.N,
            (uint32_t)p.K, (uint32_t)p.lda_bytes, (uint32_t)p.ldb_bytes, wave_u, lane);
@@ -580,29 +581,31 @@ chain_tile_kernel(const ChainParams p) {
 #pragma unroll
       for (int q = 0; q < S - 1; ++q) d.issue(lds0 + q * STAGE_BYTES, q);
       load_gen0();  // newer than the k-tile loads: only makes the waits below stricter
-      wait_loads_barrier<8 * (S - 2)>();  // k-tile 0 landed
-      KTileFrags f0, f1;
-      read_ktile_frags(smem, lane, wm, wn, f0);
-      // One k-tile step, in 8 groups of (1 load of k-tile kt+S-1, 3 fragment
-      // reads of k-tile kt+1, 2 MFMAs of k-tile kt).  A wave that issues a
-      // direct-to-LDS load stalls until the memory pipeline accepts it; with
-      // the MFMAs spread between the loads, the matrix core keeps working
-      // through those stalls instead of waiting for all 8 loads to go out.
-      // sched_barrier pins the groups (MFMAs touch no memory, so the
-      // compiler would otherwise move them freely, also across s_barrier).
-      auto step = [&](int kt, const KTileFrags& cur, KTileFrags& next) {
+      wait_loads_barrier<LPT * (S - 2)>();  // k-tile 0 landed
+      KTileFrags<NTN> f0, f1;
+#pragma unroll
+      for (int i = 0; i < RPT; ++i) read_frag_piece(smem, lane, wm, nw, i, f0);
+      // One k-tile step, in LPT groups of (1 load of k-tile kt+S-1, RPT/LPT
+      // fragment reads of k-tile kt+1, MPT/LPT MFMAs of k-tile kt).  A wave
+      // that issues a direct-to-LDS load stalls until the memory pipeline
+      // accepts it; spreading the MFMAs between the loads keeps the matrix
+      // core busy through those stalls.  sched_barrier pins the groups (MFMAs
+      // touch no memory, so the compiler would otherwise move them freely,
+      // also across s_barrier).
+      auto step = [&](int kt, const KTileFrags<NTN>& cur, KTileFrags<NTN>& next) {
         __builtin_amdgcn_sched_barrier(0);
-        wait_loads_barrier<8 * (S - 3)>();  // k-tile kt+1 landed; stage (kt-1)%S free
+        wait_loads_barrier<LPT * (S - 3)>();  // k-tile kt+1 landed; stage (kt-1)%S free
         __builtin_amdgcn_sched_barrier(0);
         const uint32_t fill = lds0 + ((kt + S - 1) % S) * STAGE_BYTES;
         const uint8_t* rd = smem + ((kt + 1) % S) * STAGE_BYTES;
 #pragma unroll
-        for (int g = 0; g < 8; ++g) {
+        for (int g = 0; g < LPT; ++g) {
           d.issue_one(fill, kt + S - 1, g);
 #pragma unroll
-          for (int i = 0; i < 3; ++i) read_frag_piece(rd, lane, wm, wn, 3 * g + i, next);
-          mma_piece<IN_DT>(cur, 2 * g, acc);
-          mma_piece<IN_DT>(cur, 2 * g + 1, acc);
+          for (int i = 0; i < RPT / LPT; ++i)
+            read_frag_piece(rd, lane, wm, nw, (RPT / LPT) * g + i, next);
+#pragma unroll
+          for (int i = 0; i < MPT / LPT; ++i) mma_piece<IN_DT>(cur, (MPT / LPT) * g + i, acc);
           __builtin_amdgcn_sched_barrier(0);
         }
       };
@@ -622,6 +625,17 @@ chain_tile_kernel(const ChainParams p) {
     // (buffer range check), so the steady-state loop issues every load and
     // store unconditionally and the compiler's count of outstanding loads
     // stays exact; the last nk % PF k-tiles run in a guarded tail.
+    static_assert(NT == 256 && NTN == 2, "register path layout");
+    Tile tl;
+    tl.ra = make_rsrc(p.a + bt * p.a_bstride, (uint32_t)p.a_bstride);
+    tl.rb = make_rsrc(p.b + bt * p.b_bstride, (uint32_t)p.b_bstride);
+    tl.row0 = row0;
+    tl.n0 = n0;
+    tl.M = p.M;
+    tl.N = p.N;
+    tl.K = p.K;
+    tl.lda = p.lda_bytes;
+    tl.ldb = p.ldb_bytes;
     StageRegs<IN_DT> R[PF];
 #pragma unroll
     for (int q = 0; q < PF; ++q) R[q].load(tl, q, t);
@@ -652,58 +666,64 @@ chain_tile_kernel(const ChainParams p) {
 
   // ---- epilogue --------------------------------------------------------------
   // Lane owns output rows m_loc(mt) = wm*64 + mt*32 + lane%32 and, for each
-  // nt, the 16 columns n_loc = wn*64 + nt*32 + acc_i(lane, v).
+  // n-subtile j, the 16 columns n_loc = nw + j*32 + acc_i(lane, v).
   const int jr = acc_j(lane);
   const int nvalid = p.N - n0 < BN ? (int)(p.N - n0) : BN;  // columns of this tile inside N
   if constexpr (EPI == kEpiLogits) {
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-      for (int nt2 = 0; nt2 < 2; ++nt2)
+      for (int j = 0; j < NTN; ++j)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) acc[mt][nt2][v] *= p.lin_scale;
+        for (int v = 0; v < 16; ++v) acc[mt][j][v] *= p.lin_scale;
   } else {
     // y = c2 * acc (log2 domain); columns past N get -inf (ragged last tile only)
     if (nvalid == BN) {
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-        for (int nt2 = 0; nt2 < 2; ++nt2)
+        for (int j = 0; j < NTN; ++j)
 #pragma unroll
-          for (int v = 0; v < 16; ++v) acc[mt][nt2][v] *= p.c2;
+          for (int v = 0; v < 16; ++v) acc[mt][j][v] *= p.c2;
     } else {
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-        for (int nt2 = 0; nt2 < 2; ++nt2)
+        for (int j = 0; j < NTN; ++j)
 #pragma unroll
           for (int v = 0; v < 16; ++v) {
-            const int n_loc = wn * 64 + nt2 * 32 + acc_i(lane, v);
-            acc[mt][nt2][v] = n_loc < nvalid ? acc[mt][nt2][v] * p.c2 : -INFINITY;
+            const int n_loc = nw + j * 32 + acc_i(lane, v);
+            acc[mt][j][v] = n_loc < nvalid ? acc[mt][j][v] * p.c2 : -INFINITY;
           }
     }
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
       float mx = -INFINITY;
 #pragma unroll
-      for (int nt2 = 0; nt2 < 2; ++nt2)
+      for (int j = 0; j < NTN; ++j)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) mx = fmaxf(mx, acc[mt][nt2][v]);
+        for (int v = 0; v < 16; ++v) mx = fmaxf(mx, acc[mt][j][v]);
       mx = wave_xor32_max(mx);
       if (lane < 32) redmax[wn * BM + wm * 64 + mt * 32 + jr] = mx;
     }
     __syncthreads();
+    auto tile_max = [&](int row) {
+      float m = redmax[row];
+#pragma unroll
+      for (int w = 1; w < WN; ++w) m = fmaxf(m, redmax[w * BM + row]);
+      return m;
+    };
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
       const int row = wm * 64 + mt * 32 + jr;
-      const float tmax = fmaxf(redmax[row], redmax[BM + row]);
+      const float tmax = tile_max(row);
       float sm = 0.0f;
 #pragma unroll
-      for (int nt2 = 0; nt2 < 2; ++nt2)
+      for (int j = 0; j < NTN; ++j)
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-          const float e = __builtin_amdgcn_exp2f(acc[mt][nt2][v] - tmax);
-          acc[mt][nt2][v] = e;
+          const float e = __builtin_amdgcn_exp2f(acc[mt][j][v] - tmax);
+          acc[mt][j][v] = e;
           sm += e;
         }
       sm = wave_xor32_sum(sm);
@@ -712,9 +732,10 @@ chain_tile_kernel(const ChainParams p) {
     __syncthreads();
     // Publish this tile's row statistics.
     if (t < BM) {
-      const float tm = fmaxf(redmax[t], redmax[BM + t]);
-      const float ts = redsum[t] + redsum[BM + t];
-      store_stat(p.partial + ((int64_t)rbg * BM + t) * p.nT + nt, tm, ts);
+      float ts = redsum[t];
+#pragma unroll
+      for (int w = 1; w < WN; ++w) ts += redsum[w * BM + t];
+      store_stat(p.partial + ((int64_t)rbg * BM + t) * p.nT + nt, tile_max(t), ts);
     }
   }
 
@@ -725,14 +746,14 @@ chain_tile_kernel(const ChainParams p) {
 #pragma unroll
   for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-    for (int nt2 = 0; nt2 < 2; ++nt2)
+    for (int j = 0; j < NTN; ++j)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int m_loc = wm * 64 + mt * 32 + jr;
-        const int n_loc = wn * 64 + nt2 * 32 + acc_i(lane, 4 * g);
+        const int n_loc = nw + j * 32 + acc_i(lane, 4 * g);
         *reinterpret_cast<f32x4*>(stg + m_loc * kStagePitch + n_loc) =
-            f32x4{acc[mt][nt2][4 * g], acc[mt][nt2][4 * g + 1], acc[mt][nt2][4 * g + 2],
-                  acc[mt][nt2][4 * g + 3]};
+            f32x4{acc[mt][j][4 * g], acc[mt][j][4 * g + 1], acc[mt][j][4 * g + 2],
+                  acc[mt][j][4 * g + 3]};
       }
 
   if constexpr (EPI == kEpiExchange) {
@@ -741,12 +762,14 @@ chain_tile_kernel(const ChainParams p) {
     __syncthreads();
     if (t == 0) rowblock_barrier(p.sync + kSyncWords * rbg, gen0, p.nT, p.err, p.spin_ticks);
     __syncthreads();
-    // Two threads per row each merge half of the row's nT (max, sum) pairs,
-    // loaded straight from the workspace in batches of 8 independent loads,
-    // then combine with their partner lane.
-    const int r = t >> 1, h = t & 1;
-    const int half = (p.nT + 1) >> 1;
-    const int q0 = h * half, q1 = q0 + half < p.nT ? q0 + half : p.nT;
+    // P = NT / BM threads per row each merge a share of the row's nT
+    // (max, sum) pairs, loaded straight from the workspace in batches of 8
+    // independent loads, then combine with their partner lanes.
+    constexpr int P = NT / BM;
+    const int r = t / P, h = t % P;
+    const int part = (p.nT + P - 1) / P;
+    const int q0 = h * part < p.nT ? h * part : p.nT;
+    const int q1 = q0 + part < p.nT ? q0 + part : p.nT;
     const float2* st = p.partial + ((int64_t)rbg * BM + r) * p.nT;
     float gm = -INFINITY, gs = 0.0f;
     for (int qb = q0; qb < q1; qb += 8) {
@@ -764,12 +787,21 @@ chain_tile_kernel(const ChainParams p) {
       gm = nm;
       gs = cs;
     }
-    // gm == -inf only for an empty half (nT == 1); its sum is 0
-    const float om = __shfl_xor(gm, 1), os = __shfl_xor(gs, 1);
-    const float M = fmaxf(gm, om);
-    const float S = (gm == -INFINITY ? 0.0f : gs * __builtin_amdgcn_exp2f(gm - M)) +
-                    (om == -INFINITY ? 0.0f : os * __builtin_amdgcn_exp2f(om - M));
-    if (h == 0) factor[r] = __builtin_amdgcn_exp2f(fmaxf(redmax[r], redmax[BM + r]) - M) / S;
+    // gm == -inf only for an empty share; its sum is 0
+#pragma unroll
+    for (int off = 1; off < P; off <<= 1) {
+      const float om = __shfl_xor(gm, off), os = __shfl_xor(gs, off);
+      const float M = fmaxf(gm, om);
+      gs = (gm == -INFINITY ? 0.0f : gs * __builtin_amdgcn_exp2f(gm - M)) +
+           (om == -INFINITY ? 0.0f : os * __builtin_amdgcn_exp2f(om - M));
+      gm = M;
+    }
+    if (h == 0) {
+      float tm = redmax[r];
+#pragma unroll
+      for (int w = 1; w < WN; ++w) tm = fmaxf(tm, redmax[w * BM + r]);
+      factor[r] = __builtin_amdgcn_exp2f(tm - gm) / gs;
+    }
   }
   __syncthreads();
 
@@ -778,7 +810,7 @@ chain_tile_kernel(const ChainParams p) {
   constexpr int EPC = 16 / OSZ;       // elements per 16-byte chunk
   constexpr int CPR = BN / EPC;       // chunks per tile row
 #pragma unroll 4
-  for (int idx = t; idx < BM * CPR; idx += NTHREADS) {
+  for (int idx = t; idx < BM * CPR; idx += NT) {
     const int row = idx / CPR, ch = idx % CPR;
     const int64_t m = row0 + row;
     const int64_t n = n0 + ch * EPC;
@@ -928,6 +960,16 @@ static int lds_bytes_for(int out_dt) {
     case DT_F32: return EpiLayout<IN_DT, DT_F32>::TOTAL;
     case DT_F16: return EpiLayout<IN_DT, DT_F16>::TOTAL;
     case DT_BF16: return EpiLayout<IN_DT, DT_BF16>::TOTAL;
+  }
+  return 0;
+}
+
+int chain_kernel_threads(int in_dt) {
+  switch (in_dt) {
+    case DT_F32: return Cfg<DT_F32>::kThreads;
+    case DT_F16: return Cfg<DT_F16>::kThreads;
+    case DT_BF16: return Cfg<DT_BF16>::kThreads;
+    case DT_FP8: return Cfg<DT_FP8>::kThreads;
   }
   return 0;
 }

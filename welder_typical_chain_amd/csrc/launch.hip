@@ -18,7 +18,7 @@ namespace {
 using namespace wtc;
 
 constexpr int kTile = 128;            // BM = BN of chain_tile_kernel
-constexpr int kThreads = 256;
+constexpr int kThreads = 256;  // the row kernels (rescale, unfused, zero fill)
 constexpr int kRescaleRowsPerWg = 4;  // rescale_rows_kernel
 constexpr int kRescaleMaxTiles = 512;
 constexpr int kExchangeMaxTiles = 64;        // row statistics staged in the 64 KiB LDS ring
@@ -159,7 +159,7 @@ int device_state(int dev, DeviceState** out) {
         const int pad = exchange_lds_pad(i, o);
         HIP_TRY(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, pad));
         int nb = 0;
-        HIP_TRY(hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, fn, kThreads, pad));
+        HIP_TRY(hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, fn, chain_kernel_threads(i), pad));
         s.occ[i][o] = nb;
       }
     s.init = true;
@@ -195,11 +195,11 @@ int default_workspace(DeviceState* s, int64_t need, void** ws, hipStream_t strea
   return WTC_OK;
 }
 
-int launch_chain(const void* kern, int64_t grid, int lds_dyn, const ChainParams& prm,
-                 hipStream_t stream) {
+int launch_chain(const void* kern, int threads, int64_t grid, int lds_dyn,
+                 const ChainParams& prm, hipStream_t stream) {
   ChainParams p = prm;
   void* args[] = {&p};
-  HIP_TRY(hipLaunchKernel(kern, dim3((unsigned)grid), dim3(kThreads), args, (size_t)lds_dyn, stream));
+  HIP_TRY(hipLaunchKernel(kern, dim3((unsigned)grid), dim3(threads), args, (size_t)lds_dyn, stream));
   return WTC_OK;
 }
 
@@ -322,11 +322,13 @@ int wtc_matmul_softmax(const void* a, const void* b, void* out, int64_t batch, i
   p.spin_ticks = kSpinTicks;
 
   if (chosen == WTC_PATH_EXCHANGE) {
-    return launch_chain(chain_kernel_symbol(in_dtype, out_dtype, kEpiExchange), grid,
+    return launch_chain(chain_kernel_symbol(in_dtype, out_dtype, kEpiExchange),
+                        chain_kernel_threads(in_dtype), grid,
                         exchange_lds_pad(in_dtype, out_dtype), p, stream);
   }
   if (chosen == WTC_PATH_SPLIT) {
-    rc = launch_chain(chain_kernel_symbol(in_dtype, out_dtype, kEpiSplit), grid, 0, p, stream);
+    rc = launch_chain(chain_kernel_symbol(in_dtype, out_dtype, kEpiSplit),
+                      chain_kernel_threads(in_dtype), grid, 0, p, stream);
     if (rc) return rc;
     uint8_t* o = p.out;
     const float2* part = p.partial;
@@ -347,7 +349,8 @@ int wtc_matmul_softmax(const void* a, const void* b, void* out, int64_t batch, i
   q.out = reinterpret_cast<uint8_t*>(logits);
   q.o_bstride = m * n * 4;
   q.ldo_bytes = n * 4;
-  rc = launch_chain(chain_kernel_symbol(in_dtype, DT_F32, kEpiLogits), grid, 0, q, stream);
+  rc = launch_chain(chain_kernel_symbol(in_dtype, DT_F32, kEpiLogits),
+                    chain_kernel_threads(in_dtype), grid, 0, q, stream);
   if (rc) return rc;
   const int64_t rows = batch * m;
   if (rows > 0x7FFFFFFFll) return fail(WTC_ERR_UNSUPPORTED, "too many rows");

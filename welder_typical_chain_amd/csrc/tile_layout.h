@@ -111,8 +111,9 @@ WTC_HD uint32_t b_unit_word(const Words& rw, int sz, int c, int w) {
 // A buffer_load ... lds instruction writes lane i's 16 bytes at
 // LDS base + 16*i: each wave instruction fills one contiguous 1 KiB block, so
 // the swizzles are realised by choosing which global chunk each lane fetches.
-// Wave w issues instructions j = 0..3 for A and for B: block b = 4w + j.
-WTC_HD constexpr int dma_block(int wave, int j) { return 4 * wave + j; }
+// With nb blocks per wave (16 / waves), wave w issues instructions
+// j = 0..nb-1 for A and for B: block b = nb*w + j.
+WTC_HD constexpr int dma_block(int wave, int j, int nb) { return nb * wave + j; }
 // A block b = rows 8b..8b+7 of the A stage; lane i lands in row 8b + i/8,
 // slot i%8, which a_lds_offset assigns to chunk slot ^ ((row>>1)&7).
 WTC_HD constexpr int dma_a_row(int b, int lane) { return 8 * b + (lane >> 3); }

@@ -36,6 +36,7 @@ const void* chain_kernel_symbol(int in_dt, int out_dt, int epi);
 const void* rescale_kernel_symbol(int out_dt);
 const void* zero_kernel_symbol();
 int chain_kernel_lds_bytes(int in_dt, int out_dt);
+int chain_kernel_threads(int in_dt);  // workgroup size of chain_tile_kernel
 
 // Unfused five-kernel baseline (matmul, row max, exp, row sum, divide).
 const void* rowmax_kernel_symbol();
