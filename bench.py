@@ -36,7 +36,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--path", default="auto", choices=["auto", "exchange", "split", "unfused"])
+    ap.add_argument("--path", default="auto", choices=["auto", "exchange", "split", "unfused", "rows"])
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="budget of the cpu_baseline sample (0 disables it)")
     ap.add_argument("--workload", default="C2", choices=["C2", "C3", "C4", "C5"],

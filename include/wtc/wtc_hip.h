@@ -45,10 +45,16 @@ extern "C" {
 #define WTC_DTYPE_FP8_E4M3 3 /* OCP e4m3 ("fn"), inputs only */
 
 /* Execution paths. */
-#define WTC_PATH_AUTO 0      /* exchange when every tile is co-resident, else split */
+#define WTC_PATH_AUTO 0      /* ROWS for 16-bit inputs with k <= 128 when there are at
+                                least as many row blocks as compute units or the tiles
+                                cannot all be co-resident; else EXCHANGE when every
+                                tile is co-resident; else SPLIT */
 #define WTC_PATH_EXCHANGE 1  /* one kernel, row statistics exchanged between tiles */
 #define WTC_PATH_SPLIT 2     /* two kernels: tile pass + row rescale (online two-pass) */
 #define WTC_PATH_UNFUSED 3   /* five kernels: matmul, max, exp, sum, divide */
+#define WTC_PATH_ROWS 4      /* one kernel, one workgroup per 128 rows over all of n:
+                                row statistics in a first pass, outputs in a second
+                                (16-bit inputs, k <= 128) */
 
 /* The fused chain.  in_dtype is one of F32/F16/BF16/FP8_E4M3; out_dtype one of
  * F32/F16/BF16.  scale_a / scale_b are the per-tensor dequantisation scales

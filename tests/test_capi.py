@@ -67,9 +67,16 @@ def test_plan_headline_and_configs(L):
     assert (rc, grid, path) == (0, 256, _lib.PATH_EXCHANGE)
     assert ws == L.wtc_matmul_softmax_workspace_size(1, 2048, 2048, 1024, 1, 1, 0)
     assert ws >= 256 + 512 * 256 + 2048 * 16 * 8
-    # C3: 64 x 256 tiles do not fit at once -> split
+    # C3: k = 128 and 64 x 16 row blocks -> one workgroup per row block
     rc, grid, path, _ = plan(L, 64, 2048, 2048, 128, 1, 1, _lib.PATH_AUTO)
+    assert (rc, grid, path) == (0, 64 * 16, _lib.PATH_ROWS)
+    rc, grid, path, _ = plan(L, 64, 2048, 2048, 128, 1, 1, _lib.PATH_SPLIT)
     assert (rc, grid, path) == (0, 64 * 256, _lib.PATH_SPLIT)
+    # the rows path needs 16-bit inputs and k <= 128
+    assert plan(L, 64, 2048, 2048, 256, 1, 1, _lib.PATH_AUTO)[2] == _lib.PATH_SPLIT
+    assert plan(L, 64, 2048, 2048, 128, _lib.DTYPE_FP8_E4M3, 1, _lib.PATH_AUTO)[2] == _lib.PATH_SPLIT
+    rc, *_ = plan(L, 1, 256, 256, 256, 1, 1, _lib.PATH_ROWS)
+    assert rc == _lib.WTC_ERR_UNSUPPORTED and b"rows path" in L.wtc_last_error()
     # C4: 8 x 256 tiles, 256 column tiles per row -> split
     rc, grid, path, _ = plan(L, 1, 1024, 32768, 4096, _lib.DTYPE_BF16, 1, _lib.PATH_AUTO)
     assert (rc, grid, path) == (0, 8 * 256, _lib.PATH_SPLIT)
@@ -134,7 +141,7 @@ def compile_chain(L, path: Path, out: Path, tiles, fused=1, errsize=4096):
 
 
 EXPECT = {  # config -> (tile_k, path chosen for the fused kernel)
-    "C1": (32, "exchange"), "C2": (64, "exchange"), "C3": (64, "split"),
+    "C1": (32, "exchange"), "C2": (64, "exchange"), "C3": (64, "rows"),
     "C4": (64, "split"), "C5": (128, "split"),
 }
 
@@ -173,10 +180,12 @@ def test_solver_and_compile_per_config(L, tmp_path, name, named):
     assert launch["runtime_scales"] == (cfg.in_dtype == "fp8")
     assert abs(launch["logit_scale"] - cfg.logit_scale) < 1e-6
     plan_json = json.loads((out / "04.kernel.plan.json").read_text())
-    assert plan_json["kernels"][0]["name"].startswith("chain_tile_kernel")
+    assert plan_json["kernels"][0]["name"].startswith("chain_rows_kernel" if path == "rows"
+                                                      else "chain_tile_kernel")
+    assert plan_json["kernels"][0]["block"][0] == (256 if cfg.in_dtype in ("f32", "fp8") else 512)
     report = dict(l.split("=", 1) for l in (out / "kernel_report.txt").read_text().splitlines()
                   if "=" in l and " " not in l.split("=", 1)[0])
-    assert int(report["launch_kernel_count"]) == (1 if path == "exchange" else 2)
+    assert int(report["launch_kernel_count"]) == (2 if path == "split" else 1)
     assert int(report["mfma_instruction_count"]) > 0
     assert int(report["scratch_instruction_count"]) == 0 and int(report["vgpr_spill_count"]) == 0
     assert int(report["kernels_without_resource_record"]) == 0

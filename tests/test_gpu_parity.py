@@ -78,12 +78,38 @@ def test_ragged_shapes(native_lib, in_dtype, out_dtype, path):
 
 
 @needs_gpu
-def test_c3_batched_attention(native_lib):
+@pytest.mark.parametrize("path", ["auto", "split"])
+def test_c3_batched_attention(native_lib, path):
     cfg = CONFIGS["C3"]
-    _announce("C3 f16 batched 8x2048x2048x128 (batch subset)")
+    _announce(f"C3 f16 batched 8x2048x2048x128 (batch subset) path={path}")
     inp = O.make_inputs(cfg, seed=0, batch=8)
-    out = run_chain(inp, cfg.in_dtype, cfg.out_dtype, batched=True)
+    out = run_chain(inp, cfg.in_dtype, cfg.out_dtype, path=path, batched=True)
     _check(cfg, inp, out, sample_rows(cfg.m, 8), batches=(0, 5, 7))
+
+
+@needs_gpu
+@pytest.mark.parametrize("in_dtype,out_dtype", [("f16", "f16"), ("bf16", "bf16"), ("f16", "f32"),
+                                                ("bf16", "f16")])
+@pytest.mark.parametrize("m,n,k", [(200, 264, 72), (128, 128, 128), (64, 4104, 8), (300, 136, 120)])
+def test_rows_path_shapes(native_lib, in_dtype, out_dtype, m, n, k):
+    """The one-workgroup-per-row-block path: ragged M / N, K below the
+    k-step, a wide row of many column tiles."""
+    cfg = ChainConfig("rows", 1, m, n, k, in_dtype, out_dtype, "normal", 0.4, logit_scale=0.6)
+    _announce(f"rows path {in_dtype}->{out_dtype} {m}x{n}x{k}")
+    inp = O.make_inputs(cfg, seed=5)
+    out = run_chain(inp, in_dtype, out_dtype, path="rows")
+    _check(cfg, inp, out, np.arange(m))
+
+
+@needs_gpu
+def test_rows_path_batched_matches_exchange(native_lib):
+    cfg = ChainConfig("rows-b", 3, 256, 512, 64, "f16", "f16", "normal", 0.5, logit_scale=0.9)
+    _announce("rows path, batch 3 256x512x64, against the oracle and the exchange path")
+    inp = O.make_inputs(cfg, seed=9)
+    rows = run_chain(inp, "f16", "f16", path="rows", batched=True)
+    _check(cfg, inp, rows, np.arange(256), batches=(0, 1, 2))
+    exch = run_chain(inp, "f16", "f16", path="exchange", batched=True)
+    assert float((rows.float() - exch.float()).abs().max()) < 2e-3
 
 
 @needs_gpu

@@ -25,9 +25,10 @@ PATH_AUTO = 0
 PATH_EXCHANGE = 1
 PATH_SPLIT = 2
 PATH_UNFUSED = 3
+PATH_ROWS = 4
 
 PATHS = {"auto": PATH_AUTO, "exchange": PATH_EXCHANGE, "split": PATH_SPLIT,
-         "unfused": PATH_UNFUSED}
+         "unfused": PATH_UNFUSED, "rows": PATH_ROWS}
 
 _c_i64 = ctypes.c_int64
 _c_p = ctypes.c_void_p

@@ -39,7 +39,7 @@ LLVM_BIN = Path(os.environ.get("ROCM_PATH", "/opt/rocm")) / "llvm" / "bin"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
-HIP_SOURCES = ["fused_matmul_softmax.hip", "unfused_chain.hip", "launch.hip"]
+HIP_SOURCES = ["fused_matmul_softmax.hip", "rowblock_softmax.hip", "unfused_chain.hip", "launch.hip"]
 CXX_SOURCES = ["chain_recognizer.cpp", "tile_solver.cpp", "compile_capi.cpp"]
 
 HIP_FLAGS = [

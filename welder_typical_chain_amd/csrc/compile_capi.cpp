@@ -19,6 +19,10 @@
 
 namespace wtc {
 
+// Workgroup sizes of the kernels (defined with the kernels in the library).
+int chain_kernel_threads(int in_dt);
+int rows_kernel_threads();
+
 static std::string library_path() {
   Dl_info info{};
   if (dladdr(reinterpret_cast<void*>(&welder_compile_typical_chain_to_nvvm), &info) && info.dli_fname)
@@ -31,6 +35,7 @@ static const char* path_name(int p) {
     case WTC_PATH_EXCHANGE: return "exchange";
     case WTC_PATH_SPLIT: return "split";
     case WTC_PATH_UNFUSED: return "unfused";
+    case WTC_PATH_ROWS: return "rows";
     default: return "auto";
   }
 }
@@ -137,6 +142,7 @@ static int compile_impl(const char* input_mlir_path, const char* out_dir, int64_
     std::string symbol_prefix;  // of the mangled name in the code object
     int64_t grid;
     int lds;
+    int block = 256;
   };
   auto chain_sym = [](int in, int out, int epi) {
     return "_ZN3wtc17chain_tile_kernelILi" + std::to_string(in) + "ELi" + std::to_string(out) +
@@ -145,16 +151,23 @@ static int compile_impl(const char* input_mlir_path, const char* out_dir, int64_
   const std::string out_t = "ILi" + std::to_string(out_code) + "E";
   std::vector<K> ks;
   const int64_t rows = spec.batch * spec.m;
-  if (path == WTC_PATH_EXCHANGE) {
+  const int tile_threads = chain_kernel_threads(in_code);
+  if (path == WTC_PATH_ROWS) {
+    ks.push_back({"chain_rows_kernel<" + kin + "," + kout + ">",
+                  "_ZN3wtc17chain_rows_kernelILi" + std::to_string(in_code) + "ELi" +
+                      std::to_string(out_code) + "E",
+                  grid, 0, rows_kernel_threads()});
+  } else if (path == WTC_PATH_EXCHANGE) {
     ks.push_back({"chain_tile_kernel<" + kin + "," + kout + ",exchange>",
-                  chain_sym(in_code, out_code, 0), grid, 82944});
+                  chain_sym(in_code, out_code, 0), grid, 82944, tile_threads});
   } else if (path == WTC_PATH_SPLIT) {
     ks.push_back({"chain_tile_kernel<" + kin + "," + kout + ",split>",
-                  chain_sym(in_code, out_code, 1), grid, 0});
+                  chain_sym(in_code, out_code, 1), grid, 0, tile_threads});
     ks.push_back({"rescale_rows_kernel<" + kout + ">", "_ZN3wtc19rescale_rows_kernel" + out_t,
                   (rows + 3) / 4, 8192});
   } else {
-    ks.push_back({"chain_tile_kernel<" + kin + ",f32,logits>", chain_sym(in_code, 0, 2), grid, 0});
+    ks.push_back({"chain_tile_kernel<" + kin + ",f32,logits>", chain_sym(in_code, 0, 2), grid, 0,
+                  tile_threads});
     ks.push_back({"rowmax_kernel", "_ZN3wtc13rowmax_kernel", rows, 16});
     ks.push_back({"expsub_kernel", "_ZN3wtc13expsub_kernel", rows, 0});
     ks.push_back({"rowsum_kernel", "_ZN3wtc13rowsum_kernel", rows, 16});
@@ -169,7 +182,8 @@ static int compile_impl(const char* input_mlir_path, const char* out_dir, int64_
        << ", \"threadTileN\": " << thread_tile_n << "},\n  \"kernels\": [\n";
   for (size_t i = 0; i < ks.size(); ++i)
     plan << "    {\"name\": \"" << ks[i].name << "\", \"grid\": [" << ks[i].grid
-         << ", 1, 1], \"block\": [256, 1, 1], \"dynamic_lds_bytes\": " << ks[i].lds << "}"
+         << ", 1, 1], \"block\": [" << ks[i].block << ", 1, 1], \"dynamic_lds_bytes\": " << ks[i].lds
+         << "}"
          << (i + 1 < ks.size() ? "," : "") << "\n";
   plan << "  ],\n  \"workspace_bytes\": " << ws << "\n}\n";
 
@@ -206,7 +220,7 @@ static int compile_impl(const char* input_mlir_path, const char* out_dir, int64_
     sspill += cell(row, "sgpr_spill_count");
     dma += cell(row, "lds_dma_loads");
     tr += cell(row, "ds_read_tr");
-    per_kernel << "kernel " << k.name << " grid=" << k.grid << " block=256";
+    per_kernel << "kernel " << k.name << " grid=" << k.grid << " block=" << k.block;
     if (row)
       per_kernel << " vgpr=" << cell(row, "vgpr_count") << " agpr=" << cell(row, "agpr_count")
                  << " sgpr=" << cell(row, "sgpr_count") << " lds_static=" << cell(row, "lds_bytes")

@@ -1,0 +1,101 @@
+// device_common.h -- device-side helpers shared by the gfx950 chain kernels
+// (fused_matmul_softmax.hip, rowblock_softmax.hip): vector types, buffer
+// descriptors and loads, direct-to-LDS loads with hand-counted waits, the
+// LDS transpose read, output packing and wave reductions.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "tile_layout.h"
+
+namespace wtc {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+constexpr uint32_t kOutOfRange = 0x80000000u;  // buffer offset that reads 0
+template <int OUT_DT> struct OutTraits;
+template <> struct OutTraits<DT_F32> { static constexpr int SZ = 4; };
+template <> struct OutTraits<DT_F16> { static constexpr int SZ = 2; };
+template <> struct OutTraits<DT_BF16> { static constexpr int SZ = 2; };
+__device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+__device__ inline u32x4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+__device__ inline u32x2 bload8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0));
+}
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+#define WTC_LDS __attribute__((address_space(3)))
+
+// Raw buffer descriptor: base, stride 0, num_records = bytes, gfx9 dword3.
+__device__ inline i32x4 raw_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  i32x4 r;
+  r[0] = (int)(uint32_t)a;
+  r[1] = (int)((uint32_t)(a >> 32) & 0xFFFFu);
+  r[2] = (int)bytes;
+  r[3] = 0x00020000;
+  return r;
+}
+
+// 16 bytes per lane into LDS at lds_base + 16*lane.  The descriptor and the
+// LDS base are wave-uniform; readfirstlane states that to the compiler so
+// the "s" operands always get scalar registers (free when they already are).
+__device__ inline void dma16(i32x4 rsrc, uint32_t voff, uint32_t lds_base) {
+  i32x4 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r[i] = __builtin_amdgcn_readfirstlane(rsrc[i]);
+  const uint32_t m = __builtin_amdgcn_readfirstlane(lds_base);
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(m), "v"(voff), "s"(r)
+               : "memory", "m0");
+}
+
+// Wait until at most N of this wave's direct-to-LDS loads are in flight and
+// its LDS reads are done, then meet the other waves.
+template <int N>
+__device__ inline void wait_loads_barrier() {
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "n"(N) : "memory");
+}
+
+typedef __fp16 h4 __attribute__((__vector_size__(4 * sizeof(__fp16))));
+
+__device__ inline u32x2 tr_read(const uint8_t* p) {
+  const h4 v = __builtin_amdgcn_ds_read_tr16_b64_v4f16((WTC_LDS h4*)(p));
+  return __builtin_bit_cast(u32x2, v);
+}
+
+// -------------------------------------------------------------------------
+// Output conversion: four f32 -> two 32-bit words of f16 / bf16 (RNE)
+// -------------------------------------------------------------------------
+template <int OUT_DT> __device__ inline void pack4(const f32x4& x, uint32_t* w0, uint32_t* w1);
+template <> __device__ inline void pack4<DT_F16>(const f32x4& x, uint32_t* w0, uint32_t* w1) {
+  const float x0 = x[0], x1 = x[1], x2 = x[2], x3 = x[3];
+  *w0 = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x0) |
+        ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x1) << 16);
+  *w1 = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x2) |
+        ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x3) << 16);
+}
+template <> __device__ inline void pack4<DT_BF16>(const f32x4& x, uint32_t* w0, uint32_t* w1) {
+  const float x0 = x[0], x1 = x[1], x2 = x[2], x3 = x[3];
+  *w0 = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x0) |
+        ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x1) << 16);
+  *w1 = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x2) |
+        ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x3) << 16);
+}
+
+__device__ inline float wave_xor32_max(float x) { return fmaxf(x, __shfl_xor(x, 32)); }
+__device__ inline float wave_xor32_sum(float x) { return x + __shfl_xor(x, 32); }
+
+
+}  // namespace wtc

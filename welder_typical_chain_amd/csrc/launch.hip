@@ -80,7 +80,7 @@ int check_args(int64_t batch, int64_t m, int64_t n, int64_t k, int in_dt, int ou
     return fail(WTC_ERR_ARG, "negative extent");
   if (!valid_in(in_dt)) return fail(WTC_ERR_ARG, "unsupported in_dtype");
   if (!valid_out(out_dt)) return fail(WTC_ERR_ARG, "unsupported out_dtype");
-  if (path < WTC_PATH_AUTO || path > WTC_PATH_UNFUSED)
+  if (path < WTC_PATH_AUTO || path > WTC_PATH_ROWS)
     return fail(WTC_ERR_ARG, "unknown path");
   if ((k * dtype_bytes(in_dt)) % 16 != 0)
     return fail(WTC_ERR_ARG, "k * element bytes must be a multiple of 16");
@@ -104,7 +104,16 @@ int plan_impl(int64_t batch, int64_t m, int64_t n, int64_t k, int in_dt, int out
   const int64_t nT = ceil_div(n, kTile);
   const int64_t rbs = batch * ceil_div(m, kTile);
   const bool fits = tiles <= capacity && nT <= kExchangeMaxTiles && rbs <= kMaxSyncRowBlocks;
-  if (p == WTC_PATH_AUTO) p = fits ? WTC_PATH_EXCHANGE : WTC_PATH_SPLIT;
+  const bool rows_ok = (in_dt == DT_F16 || in_dt == DT_BF16) && k <= rows_kernel_max_k();
+  if (p == WTC_PATH_AUTO) {
+    if (rows_ok && (!fits || rbs >= (int64_t)cu_count))
+      p = WTC_PATH_ROWS;
+    else
+      p = fits ? WTC_PATH_EXCHANGE : WTC_PATH_SPLIT;
+  }
+  if (p == WTC_PATH_ROWS && !rows_ok)
+    return fail(WTC_ERR_UNSUPPORTED, "rows path needs 16-bit inputs and k <= " +
+                                         std::to_string(rows_kernel_max_k()));
   if (p == WTC_PATH_EXCHANGE && tiles > capacity)
     return fail(WTC_ERR_UNSUPPORTED,
                 "exchange path needs every tile co-resident: " + std::to_string(tiles) +
@@ -114,7 +123,7 @@ int plan_impl(int64_t batch, int64_t m, int64_t n, int64_t k, int in_dt, int out
   if (p == WTC_PATH_SPLIT && ceil_div(n, kTile) > kRescaleMaxTiles)
     return fail(WTC_ERR_UNSUPPORTED, "split path supports n <= 65536");
   if (tiles > 0x7FFFFFFFll) return fail(WTC_ERR_UNSUPPORTED, "too many tiles for one grid");
-  if (grid) *grid = tiles;
+  if (grid) *grid = p == WTC_PATH_ROWS ? rbs : tiles;
   if (chosen) *chosen = p;
   if (ws_bytes) *ws_bytes = ws_layout(batch, m, n, p).total;
   return WTC_OK;
@@ -321,6 +330,10 @@ int wtc_matmul_softmax(const void* a, const void* b, void* out, int64_t batch, i
   p.err = reinterpret_cast<uint32_t*>(wsb);
   p.spin_ticks = kSpinTicks;
 
+  if (chosen == WTC_PATH_ROWS) {
+    return launch_chain(rows_kernel_symbol(in_dtype, out_dtype), rows_kernel_threads(), grid, 0,
+                        p, stream);
+  }
   if (chosen == WTC_PATH_EXCHANGE) {
     return launch_chain(chain_kernel_symbol(in_dtype, out_dtype, kEpiExchange),
                         chain_kernel_threads(in_dtype), grid,

@@ -38,6 +38,11 @@ const void* zero_kernel_symbol();
 int chain_kernel_lds_bytes(int in_dt, int out_dt);
 int chain_kernel_threads(int in_dt);  // workgroup size of chain_tile_kernel
 
+// One workgroup per 128-row block, two passes over N (K <= rows_kernel_max_k()).
+const void* rows_kernel_symbol(int in_dt, int out_dt);
+int rows_kernel_threads();
+int rows_kernel_max_k();
+
 // Unfused five-kernel baseline (matmul, row max, exp, row sum, divide).
 const void* rowmax_kernel_symbol();
 const void* expsub_kernel_symbol();
