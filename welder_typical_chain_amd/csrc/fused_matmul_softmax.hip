@@ -71,8 +71,8 @@ template <int IN_DT, int OUT_DT> struct EpiLayout {
   static constexpr int RING = Cfg<IN_DT>::kRingBytes;
   static constexpr int UNION = STAGING > RING ? STAGING : RING;
   static constexpr int RED_OFF = (UNION + 255) / 256 * 256;
-  // redmax[kWavesN][BM], redsum[kWavesN][BM], factor[BM]  (floats)
-  static constexpr int TOTAL = RED_OFF + (2 * Cfg<IN_DT>::kWavesN + 1) * BM * 4;
+  // wstat[kWavesN][BM] (float2), factor[kWavesN][BM] (float)
+  static constexpr int TOTAL = RED_OFF + 3 * Cfg<IN_DT>::kWavesN * BM * 4;
 };
 
 // -------------------------------------------------------------------------
@@ -368,12 +368,17 @@ __device__ inline float2 load_stat(const float2* p) {
   return make_float2(__builtin_bit_cast(float, lo), __builtin_bit_cast(float, hi));
 }
 
-// Arrival of one tile at its row block's counter (called by one thread after
-// the tile's statistics are stored).  Returns once every tile of the row
-// block has arrived, or after spin_ticks of the 100 MHz clock (then err gets
-// bit 0 and the tile goes on with what it sees, so the kernel always drains).
-// The last arriver resets the counter and bumps the generation word, so the
-// protocol keeps no per-launch state and survives graph replay.
+// Row-block barrier of the exchange path (called by one thread per tile once
+// the tile's statistics are stored).  Per row block the workspace holds an
+// arrival counter and a generation word, each in a cache line of its own
+// (kSyncWords apart per row block): polls of the generation word never
+// contend with the arrivals' atomic adds on the counter.  Each tile adds 1 to
+// the counter; the one that brings it to nT resets it to 0 and bumps the
+// generation; the others poll the generation until it differs from g0, the
+// value read at kernel start (it cannot move before this tile arrives, so
+// reading it early keeps it off the critical path).  The protocol keeps no
+// per-launch host state, so it survives graph replay, and the counter is
+// back at 0 after every launch, so a workspace may be reused for any shape.
 //
 // Memory ordering without cache maintenance: every word that crosses
 // workgroups here (statistics, counter, generation) is read and written only
@@ -385,15 +390,13 @@ __device__ inline float2 load_stat(const float2* p) {
 // Agent-scope release/acquire fences would write back / invalidate the whole
 // L2 of the XCD, which costs far more than the exchange itself.
 //
-// The counter and the generation word of a row block sit in cache lines of
-// their own (kSyncWords apart per row block): polls of one row block do not
-// contend with the arrivals of another, nor with their own counter.
-// g0 is the generation word as read at kernel start (it cannot change before
-// this tile arrives, so reading it early keeps it off the critical path).
-__device__ inline void rowblock_barrier(uint32_t* cnt_gen, uint32_t g0, int nT, uint32_t* err,
+// Returns once every tile of the row block has arrived, or after spin_ticks
+// of the 100 MHz clock (then err gets bit 0 and the tile goes on with what it
+// sees, so the kernel always drains).
+__device__ inline void rowblock_barrier(uint32_t* sync, uint32_t g0, int nT, uint32_t* err,
                                         uint64_t spin_ticks) {
-  uint32_t* cnt = cnt_gen;
-  uint32_t* gen = cnt_gen + kSyncWords / 2;
+  uint32_t* cnt = sync + kSyncCnt;
+  uint32_t* gen = sync + kSyncGen;
   const uint32_t old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   if (old == (uint32_t)(nT - 1)) {
     __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -427,9 +430,8 @@ chain_tile_kernel(const ChainParams p) {
   constexpr int WN = C::kWavesN;
   constexpr int NTN = C::kNT;
   __shared__ __attribute__((aligned(16))) uint8_t smem[L::TOTAL];
-  float* redmax = reinterpret_cast<float*>(smem + L::RED_OFF);  // [WN][BM]
-  float* redsum = redmax + WN * BM;                              // [WN][BM]
-  float* factor = redsum + WN * BM;                              // [BM]
+  float2* wstat = reinterpret_cast<float2*>(smem + L::RED_OFF);  // [WN][BM] wave (max, sum)
+  float* factor = reinterpret_cast<float*>(wstat + WN * BM);     // [WN][BM]
 
   const int t = threadIdx.x;
   const int lane = t & 63;
@@ -457,7 +459,7 @@ chain_tile_kernel(const ChainParams p) {
   uint32_t gen0 = 0;
   auto load_gen0 = [&]() {
     if constexpr (EPI == kEpiExchange)
-      gen0 = __hip_atomic_load(p.sync + kSyncWords * rbg + kSyncWords / 2, __ATOMIC_RELAXED,
+      gen0 = __hip_atomic_load(p.sync + kSyncWords * rbg + kSyncGen, __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
   };
 
@@ -580,7 +582,11 @@ chain_tile_kernel(const ChainParams p) {
 
   // ---- epilogue --------------------------------------------------------------
   // Lane owns output rows m_loc(mt) = wm*64 + mt*32 + lane%32 and, for each
-  // n-subtile j, the 16 columns n_loc = nw + j*32 + acc_i(lane, v).
+  // n-subtile j, the 16 columns n_loc = nw + j*32 + acc_i(lane, v).  Each
+  // wave normalises its exponentials against the max of its own columns
+  // (wave max m_w, sum s_w per row, kept in LDS); the tile's statistics and
+  // the final scale factors are combined from those, so one LDS exchange
+  // serves both.
   const int jr = acc_j(lane);
   const int nvalid = p.N - n0 < BN ? (int)(p.N - n0) : BN;  // columns of this tile inside N
   if constexpr (EPI == kEpiLogits) {
@@ -618,44 +624,46 @@ chain_tile_kernel(const ChainParams p) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) mx = fmaxf(mx, acc[mt][j][v]);
       mx = wave_xor32_max(mx);
-      if (lane < 32) redmax[wn * BM + wm * 64 + mt * 32 + jr] = mx;
-    }
-    __syncthreads();
-    auto tile_max = [&](int row) {
-      float m = redmax[row];
-#pragma unroll
-      for (int w = 1; w < WN; ++w) m = fmaxf(m, redmax[w * BM + row]);
-      return m;
-    };
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      const int row = wm * 64 + mt * 32 + jr;
-      const float tmax = tile_max(row);
+      const float base = mx == -INFINITY ? 0.0f : mx;  // every column of this wave past N
       float sm = 0.0f;
 #pragma unroll
       for (int j = 0; j < NTN; ++j)
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-          const float e = __builtin_amdgcn_exp2f(acc[mt][j][v] - tmax);
+          const float e = __builtin_amdgcn_exp2f(acc[mt][j][v] - base);
           acc[mt][j][v] = e;
           sm += e;
         }
       sm = wave_xor32_sum(sm);
-      if (lane < 32) redsum[wn * BM + row] = sm;
+      if (lane < 32) wstat[wn * BM + wm * 64 + mt * 32 + jr] = make_float2(mx, sm);
     }
-    __syncthreads();
-    // Publish this tile's row statistics.
-    if (t < BM) {
-      float ts = redsum[t];
+  }
+
+  // The tile's statistics of row r from the WN wave entries.
+  auto tile_stat = [&](int r) {
+    float tm = wstat[r].x;
 #pragma unroll
-      for (int w = 1; w < WN; ++w) ts += redsum[w * BM + t];
-      store_stat(p.partial + ((int64_t)rbg * BM + t) * p.nT + nt, tile_max(t), ts);
+    for (int w = 1; w < WN; ++w) tm = fmaxf(tm, wstat[w * BM + r].x);
+    float ts = 0.0f;
+#pragma unroll
+    for (int w = 0; w < WN; ++w) {
+      const float2 e = wstat[w * BM + r];
+      ts += e.x == -INFINITY ? 0.0f : e.y * __builtin_amdgcn_exp2f(e.x - tm);
+    }
+    return make_float2(tm, ts);
+  };
+  if constexpr (EPI != kEpiLogits) {
+    __syncthreads();  // the wave statistics are in place
+    // Publish this tile's row statistics (partial[row block][row][column tile]).
+    if (t < BM) {
+      const float2 st = tile_stat(t);
+      store_stat(p.partial + ((int64_t)rbg * BM + t) * p.nT + nt, st.x, st.y);
     }
   }
 
   // Stage the tile in LDS as f32 (the ring is free: every load has landed
-  // and every wave is past the last k-tile).  For the exchange path this
-  // happens before the row-block wait, so the wait hides it.
+  // and every wave is past the last k-tile).  This overlaps the statistics
+  // stores and, on the exchange path, precedes the row-block wait.
   float* stg = reinterpret_cast<float*>(smem);
 #pragma unroll
   for (int mt = 0; mt < 2; ++mt)
@@ -670,51 +678,56 @@ chain_tile_kernel(const ChainParams p) {
                   acc[mt][j][4 * g + 3]};
       }
 
-  if constexpr (EPI == kEpiExchange) {
-    // statistics stores complete before this tile is counted
-    if (t < BM) __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (t == 0) rowblock_barrier(p.sync + kSyncWords * rbg, gen0, p.nT, p.err, p.spin_ticks);
-    __syncthreads();
-    // P = NT / BM threads per row each merge a share of the row's nT
-    // (max, sum) pairs, loaded straight from the workspace in batches of 8
-    // independent loads, then combine with their partner lanes.
-    constexpr int P = NT / BM;
+  if constexpr (EPI != kEpiLogits) {
+    if constexpr (EPI == kEpiExchange) {
+      if (t < BM) __builtin_amdgcn_s_waitcnt(0);  // statistics stores complete before this tile is counted
+      __syncthreads();
+      if (t == 0) rowblock_barrier(p.sync + kSyncWords * rbg, gen0, p.nT, p.err, p.spin_ticks);
+    }
+    constexpr int P = NT / BM;  // threads per row (== WN)
+    static_assert(P == WN, "one thread per (row, wave column slice)");
     const int r = t / P, h = t % P;
-    const int part = (p.nT + P - 1) / P;
-    const int q0 = h * part < p.nT ? h * part : p.nT;
-    const int q1 = q0 + part < p.nT ? q0 + part : p.nT;
-    const float2* st = p.partial + ((int64_t)rbg * BM + r) * p.nT;
-    float gm = -INFINITY, gs = 0.0f;
-    for (int qb = q0; qb < q1; qb += 8) {
-      float2 v[8];
+    if constexpr (EPI == kEpiExchange) {
+      __syncthreads();  // the row block's statistics are all in place
+      // The P threads of a row each merge a share of its nT (max, sum)
+      // pairs, loaded straight from the workspace in batches of 8
+      // independent loads, then combine with their partner lanes.
+      const int part = (p.nT + P - 1) / P;
+      const int q0 = h * part < p.nT ? h * part : p.nT;
+      const int q1 = q0 + part < p.nT ? q0 + part : p.nT;
+      const float2* st = p.partial + ((int64_t)rbg * BM + r) * p.nT;
+      float gm = -INFINITY, gs = 0.0f;
+      for (int qb = q0; qb < q1; qb += 8) {
+        float2 v[8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u)
-        v[u] = qb + u < q1 ? load_stat(st + qb + u) : make_float2(-INFINITY, 0.0f);
-      float cm = v[0].x;
+        for (int u = 0; u < 8; ++u)
+          v[u] = qb + u < q1 ? load_stat(st + qb + u) : make_float2(-INFINITY, 0.0f);
+        float cm = v[0].x;
 #pragma unroll
-      for (int u = 1; u < 8; ++u) cm = fmaxf(cm, v[u].x);
-      const float nm = fmaxf(gm, cm);
-      float cs = gs * __builtin_amdgcn_exp2f(gm - nm);
+        for (int u = 1; u < 8; ++u) cm = fmaxf(cm, v[u].x);
+        const float nm = fmaxf(gm, cm);
+        float cs = gs * __builtin_amdgcn_exp2f(gm - nm);
 #pragma unroll
-      for (int u = 0; u < 8; ++u) cs += v[u].y * __builtin_amdgcn_exp2f(v[u].x - nm);
-      gm = nm;
-      gs = cs;
-    }
-    // gm == -inf only for an empty share; its sum is 0
+        for (int u = 0; u < 8; ++u) cs += v[u].y * __builtin_amdgcn_exp2f(v[u].x - nm);
+        gm = nm;
+        gs = cs;
+      }
+      // gm == -inf only for an empty share; its sum is 0
 #pragma unroll
-    for (int off = 1; off < P; off <<= 1) {
-      const float om = __shfl_xor(gm, off), os = __shfl_xor(gs, off);
-      const float M = fmaxf(gm, om);
-      gs = (gm == -INFINITY ? 0.0f : gs * __builtin_amdgcn_exp2f(gm - M)) +
-           (om == -INFINITY ? 0.0f : os * __builtin_amdgcn_exp2f(om - M));
-      gm = M;
-    }
-    if (h == 0) {
-      float tm = redmax[r];
-#pragma unroll
-      for (int w = 1; w < WN; ++w) tm = fmaxf(tm, redmax[w * BM + r]);
-      factor[r] = __builtin_amdgcn_exp2f(tm - gm) / gs;
+      for (int off = 1; off < P; off <<= 1) {
+        const float om = __shfl_xor(gm, off), os = __shfl_xor(gs, off);
+        const float M = fmaxf(gm, om);
+        gs = (gm == -INFINITY ? 0.0f : gs * __builtin_amdgcn_exp2f(gm - M)) +
+             (om == -INFINITY ? 0.0f : os * __builtin_amdgcn_exp2f(om - M));
+        gm = M;
+      }
+      // thread (r, h) owns the factor of row r, column slice of wave h
+      const float mw = wstat[h * BM + r].x;
+      factor[h * BM + r] = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - gm) / gs;
+    } else {
+      // split: exponentials relative to the tile max, as the statistics say
+      const float mw = wstat[h * BM + r].x;
+      factor[h * BM + r] = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - tile_stat(r).x);
     }
   }
   __syncthreads();
@@ -729,7 +742,7 @@ chain_tile_kernel(const ChainParams p) {
     const int64_t m = row0 + row;
     const int64_t n = n0 + ch * EPC;
     if (m < p.M && n < p.N) {
-      const float f = EPI == kEpiExchange ? factor[row] : 1.0f;
+      const float f = EPI == kEpiLogits ? 1.0f : factor[(ch * EPC / (32 * NTN)) * BM + row];
       const float* src = stg + row * kStagePitch + ch * EPC;
       const f32x4 x0 = *reinterpret_cast<const f32x4*>(src) * f;
       if constexpr (OSZ == 4) {
@@ -766,7 +779,7 @@ rescale_rows_kernel(uint8_t* __restrict__ out, const float2* __restrict__ partia
     bt = grow / M;
     m = grow % M;
     const int64_t rbg = bt * nRB + m / BM;
-    const float2* st = partial + (rbg * BM + (m % BM)) * nT;
+    const float2* st = partial + (rbg * BM + (m % BM)) * nT;  // [row][column tile]
     float gm = -INFINITY;
     for (int q = lane; q < nT; q += 64) gm = fmaxf(gm, st[q].x);
 #pragma unroll

@@ -10,9 +10,12 @@ namespace wtc {
 
 enum : int { kEpiExchange = 0, kEpiSplit = 1, kEpiLogits = 2 };
 
-// 32-bit words of workspace per row block for the exchange counter (word 0)
-// and generation (word kSyncWords/2): 256 bytes, two cache lines.
+// 32-bit words of workspace per row block for the exchange: the arrival
+// counter at word kSyncCnt and the generation word at kSyncGen, each in a
+// 128-byte line of its own.
 constexpr int kSyncWords = 64;
+constexpr int kSyncCnt = 0;
+constexpr int kSyncGen = 32;
 
 struct ChainParams {
   const uint8_t* a;
