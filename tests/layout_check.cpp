@@ -249,8 +249,81 @@ static void run_dma16() {
   CHECK(cr.worst == 1, "[dma16] tr reads conflict\n");
 }
 
+// DMA staging + ds_read_b64_tr_b8 operand path of the fp8 kernels: the B
+// operand bytes of every lane must be the column and k the A operand of the
+// same lane pairs with.
+static void run_dma8() {
+  const int KE = 128;  // fp8 per k-tile
+  std::vector<uint8_t> A(BM * KE), B(KE * BN);
+  for (int m = 0; m < BM; ++m)
+    for (int k = 0; k < KE; ++k) A[m * KE + k] = (uint8_t)((m * 7 + k * 3) % 251);
+  for (int k = 0; k < KE; ++k)
+    for (int n = 0; n < BN; ++n) B[k * BN + n] = (uint8_t)((k * 5 + n * 11) % 253);
+  std::vector<uint8_t> sa(BM * 128), sb(KE * 128);
+  std::vector<int> ca(sa.size(), 0), cb(sb.size(), 0);
+  for (int w = 0; w < 8; ++w)
+    for (int j = 0; j < 2; ++j) {
+      const int b = dma_block(w, j, 2);
+      for (int i = 0; i < 64; ++i) {
+        const int row = dma_a_row(b, i), c = dma_a_chunk(b, i);
+        const int dst = b * 1024 + 16 * i;
+        CHECK(a_lds_offset(row, c) == dst, "[dma8] A lane %d of block %d lands off-layout\n", i, b);
+        std::memcpy(&sa[dst], &A[row * KE + c * 16], 16);
+        for (int x = 0; x < 16; ++x) ca[dst + x]++;
+        const int kr = dma8_b_row(b, i), cc = dma8_b_chunk(b, i);
+        CHECK(btr8_offset(kr, 16 * cc) == dst, "[dma8] B lane %d of block %d lands off-layout\n", i, b);
+        std::memcpy(&sb[dst], &B[kr * BN + 16 * cc], 16);
+        for (int x = 0; x < 16; ++x) cb[dst + x]++;
+      }
+    }
+  for (size_t i = 0; i < ca.size(); ++i) CHECK(ca[i] == 1 && cb[i] == 1, "[dma8] LDS byte %zu coverage\n", i);
+  Conflicts cr;
+  for (int wave = 0; wave < 8; ++wave) {
+    const int wm = wave >> 2, wn = wave & 3;
+    const int nb = wn * 32;
+    for (int s = 0; s < 2; ++s) {
+      uint8_t bop[64][32], aop[2][64][32];
+      for (int q = 0; q < 4; ++q) {
+        uint8_t src[64][8];
+        std::vector<int> addrs;
+        for (int l = 0; l < 64; ++l) {
+          const int off = btr8_offset(btr8_k(s, q, l), btr8_n(nb, l));
+          std::memcpy(src[l], &sb[off], 8);
+          addrs.push_back(off);
+          if ((l & 31) == 31) {
+            cr.phase(addrs, 8);
+            addrs.clear();
+          }
+        }
+        for (int l = 0; l < 64; ++l)  // the transpose, as measured on gfx950
+          for (int r = 0; r < 8; ++r) bop[l][8 * q + r] = src[16 * (l / 16) + 2 * r + (l % 16) / 8][(l % 16) % 8];
+      }
+      for (int mt = 0; mt < 2; ++mt)
+        for (int l = 0; l < 64; ++l)
+          for (int hh = 0; hh < 2; ++hh) {
+            const int row = wm * 64 + mt * 32 + (l & 31);
+            const int chunk = 4 * s + 2 * (l >> 5) + hh;
+            std::memcpy(&aop[mt][l][16 * hh], &sa[a_lds_offset(row, chunk)], 16);
+          }
+      for (int l = 0; l < 64; ++l)
+        for (int e = 0; e < 32; ++e) {
+          const int k = 64 * s + 32 * (l >> 5) + e, n = nb + (l & 31);
+          CHECK(bop[l][e] == B[k * BN + n], "[dma8] B operand lane %d byte %d: got %d want %d\n", l, e, bop[l][e],
+                B[k * BN + n]);
+          for (int mt = 0; mt < 2; ++mt) {
+            const int row = wm * 64 + mt * 32 + (l & 31);
+            CHECK(aop[mt][l][e] == A[row * KE + k], "[dma8] A operand lane %d byte %d\n", l, e);
+          }
+        }
+    }
+  }
+  std::printf("[dma8] tr8-read bank-conflict ways: %d\n", cr.worst);
+  CHECK(cr.worst == 1, "[dma8] tr8 reads conflict\n");
+}
+
 int main() {
   run_dma16();
+  run_dma8();
   run(2, "f16/bf16");
   run(1, "fp8");
   run(4, "f32");

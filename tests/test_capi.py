@@ -154,7 +154,7 @@ def test_solver_and_compile_per_config(L, tmp_path, name, named):
     rc, tiles, err = solve(L, src, tmp_path)
     assert rc == 0, err
     tile_k, path = EXPECT[name]
-    assert tiles == [128, 128, tile_k, 2, 32]
+    assert tiles == [128, 128, tile_k, 2, 32 if cfg.in_dtype == "f32" else 16]
     summary = json.loads((tmp_path / "best_summary.json").read_text())
     assert {k: summary["problem"][k] for k in "mnk"} == {"m": cfg.m, "n": cfg.n, "k": cfg.k}
     assert {"smemBytes", "numSM", "warpSize", "elementBytes"} <= set(summary["arch"])
@@ -182,7 +182,7 @@ def test_solver_and_compile_per_config(L, tmp_path, name, named):
     plan_json = json.loads((out / "04.kernel.plan.json").read_text())
     assert plan_json["kernels"][0]["name"].startswith("chain_rows_kernel" if path == "rows"
                                                       else "chain_tile_kernel")
-    assert plan_json["kernels"][0]["block"][0] == (256 if cfg.in_dtype in ("f32", "fp8") else 512)
+    assert plan_json["kernels"][0]["block"][0] == (256 if cfg.in_dtype == "f32" else 512)
     report = dict(l.split("=", 1) for l in (out / "kernel_report.txt").read_text().splitlines()
                   if "=" in l and " " not in l.split("=", 1)[0])
     assert int(report["launch_kernel_count"]) == (2 if path == "split" else 1)
@@ -202,7 +202,7 @@ def test_solver_and_compile_per_config(L, tmp_path, name, named):
 
 def test_compile_unfused_baseline(L, tmp_path):
     src = write_chain(tmp_path, CONFIGS["C2"])
-    rc, err = compile_chain(L, src, tmp_path / "baseline", [128, 128, 64, 2, 32], fused=0)
+    rc, err = compile_chain(L, src, tmp_path / "baseline", [128, 128, 64, 2, 16], fused=0)
     assert rc == 0, err
     plan_json = json.loads((tmp_path / "baseline" / "04.kernel.plan.json").read_text())
     assert [k["name"].split("<")[0] for k in plan_json["kernels"]] == [
@@ -212,18 +212,18 @@ def test_compile_unfused_baseline(L, tmp_path):
 
 def test_compile_error_codes(L, tmp_path):
     src = write_chain(tmp_path, CONFIGS["C2"])
-    assert compile_chain(L, src, tmp_path / "o", [0, 128, 64, 2, 32])[0] == 1
+    assert compile_chain(L, src, tmp_path / "o", [0, 128, 64, 2, 16])[0] == 1
     err = ctypes.create_string_buffer(64)
-    assert L.welder_compile_typical_chain_to_nvvm(b"", b"x", b"", b"", 128, 128, 64, 2, 32, 1, 1, 0,
+    assert L.welder_compile_typical_chain_to_nvvm(b"", b"x", b"", b"", 128, 128, 64, 2, 16, 1, 1, 0,
                                                   err, 64) == 1
     assert err.value
-    rc, msg = compile_chain(L, src, tmp_path / "o", [64, 64, 64, 2, 32])  # no such variant
+    rc, msg = compile_chain(L, src, tmp_path / "o", [64, 64, 64, 2, 16])  # no such variant
     assert rc == 2 and b"no gfx950 kernel variant" in msg
     bad = tmp_path / "bad.mlir"
     bad.write_text("module { func.func @main() { return } }")
-    rc, msg = compile_chain(L, bad, tmp_path / "o", [128, 128, 64, 2, 32])
+    rc, msg = compile_chain(L, bad, tmp_path / "o", [128, 128, 64, 2, 16])
     assert rc == 2 and msg
-    rc, msg = compile_chain(L, tmp_path / "missing.mlir", tmp_path / "o", [128, 128, 64, 2, 32])
+    rc, msg = compile_chain(L, tmp_path / "missing.mlir", tmp_path / "o", [128, 128, 64, 2, 16])
     assert rc == 2
 
 

@@ -70,6 +70,12 @@ __device__ inline void wait_loads_barrier() {
 
 typedef __fp16 h4 __attribute__((__vector_size__(4 * sizeof(__fp16))));
 
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+// ds_read_b64_tr_b8: see tile_layout.h (btr8_k / btr8_n) for the lane mapping.
+__device__ inline u32x2 tr8_read(const uint8_t* p) {
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr8_b64_v2i32((WTC_LDS i32x2*)(p)));
+}
+
 __device__ inline u32x2 tr_read(const uint8_t* p) {
   const h4 v = __builtin_amdgcn_ds_read_tr16_b64_v4f16((WTC_LDS h4*)(p));
   return __builtin_bit_cast(u32x2, v);

@@ -34,6 +34,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "device_common.h"
 #include "tile_layout.h"
 #include "wtc_kernels.h"
@@ -46,12 +48,12 @@ constexpr int BN = 128;
 constexpr int A_STAGE_BYTES = BM * kKTileBytes;                  // 16 KiB
 constexpr int STAGE_BYTES = A_STAGE_BYTES + BN * kKTileBytes;    // 32 KiB
 
-// Per input type: 16-bit inputs stream through a 4-stage ring filled by
-// direct-to-LDS loads and run 8 waves (2 per SIMD: while one waits to issue
-// a load, the other issues MFMAs), each owning a 64x32 block; fp8 / f32 go
+// Per input type: 16-bit and fp8 inputs stream through a 4-stage ring filled
+// by direct-to-LDS loads and run 8 waves (2 per SIMD: while one waits to
+// issue a load, the other issues MFMAs), each owning a 64x32 block; f32 goes
 // through a 2-stage ring filled from registers with 4 waves of 64x64.
 template <int IN_DT> struct Cfg {
-  static constexpr bool kDma = IN_DT == DT_F16 || IN_DT == DT_BF16;
+  static constexpr bool kDma = IN_DT == DT_F16 || IN_DT == DT_BF16 || IN_DT == DT_FP8;
   static constexpr int kWavesN = kDma ? 4 : 2;          // waves along N (2 along M)
   static constexpr int kWaves = 2 * kWavesN;
   static constexpr int kThreads = 64 * kWaves;
@@ -155,8 +157,10 @@ template <int IN_DT> struct StageRegs {
 // past M and k-rows past K fall outside the descriptors' ranges by
 // themselves; columns past N are parked at kOutOfRange, which stays out of
 // range for every k-tile (kt*b_step < 2^31).
-template <int NB>  // 1 KiB blocks per operand per wave
+template <int IN_DT, int NB>  // 1 KiB blocks per operand per wave
 struct DmaPlan {
+  static constexpr int SZ = dtype_bytes(IN_DT);
+  static constexpr int KE = kKTileBytes / SZ;  // k-rows of B per k-tile
   i32x4 ra, rb;
   uint32_t a_base[NB], b_base[NB];
   uint32_t a_chunk[NB];  // byte offset of the lane's A chunk inside a k-tile
@@ -175,16 +179,19 @@ struct DmaPlan {
       ra[i] = __builtin_amdgcn_readfirstlane(ra_v[i]);
       rb[i] = __builtin_amdgcn_readfirstlane(rb_v[i]);
     }
-    k_bytes = K * 2;
-    b_step = 64 * ldb;
+    k_bytes = K * SZ;
+    b_step = KE * ldb;
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
       const int blk = dma_block(wave_u, j, NB);
       const uint32_t row = row0 + (uint32_t)dma_a_row(blk, lane);
       a_chunk[j] = (uint32_t)dma_a_chunk(blk, lane) * kChunkBytes;
       a_base[j] = row < M ? row * lda + a_chunk[j] : kOutOfRange;
-      const uint32_t n = n0 + 8u * (uint32_t)dma_b_chunk(blk, lane);
-      b_base[j] = n < N ? (uint32_t)dma_b_row(blk, lane) * ldb + n * 2 : kOutOfRange;
+      // a B chunk is 16 bytes: 8 columns of 16-bit data, 16 of fp8
+      const uint32_t krow = SZ == 1 ? (uint32_t)dma8_b_row(blk, lane) : (uint32_t)dma_b_row(blk, lane);
+      const uint32_t n = n0 + (SZ == 1 ? 16u * (uint32_t)dma8_b_chunk(blk, lane)
+                                       : 8u * (uint32_t)dma_b_chunk(blk, lane));
+      b_base[j] = n < N ? krow * ldb + n * SZ : kOutOfRange;
       lds_a[j] = blk * 1024;
       lds_b[j] = A_STAGE_BYTES + blk * 1024;
     }
@@ -355,6 +362,43 @@ __device__ inline void mma_piece(const KTileFrags<NTN>& f, int i, f32x16 (&acc)[
   }
 }
 
+// fp8 (e4m3) operands of one k-tile (128 k = 2 MFMA k-steps of 64) for one
+// wave of 64 rows x 32 columns: A [step][m-subtile][16-byte half],
+// B [step][8-byte transpose read].
+struct KTileFrags8 {
+  u32x4 a[2][2][2];
+  u32x2 b[2][4];
+};
+
+// LDS read i (0..15) of an fp8 k-tile's fragments: for k-step s = i / 8,
+// reads 0-3 are the A halves (ds_read_b128: chunks 4s + 2(lane/32) + 0/1
+// of m-subtiles 0, 1), reads 4-7 the four ds_read_b64_tr_b8 of B.
+__device__ inline void read_frag_piece8(const uint8_t* stage, int lane, int wm, int nw, int i,
+                                        KTileFrags8& f) {
+  const int s = i / 8, u = i % 8;
+  if (u < 4) {
+    const int mt = u >> 1, hh = u & 1;
+    f.a[s][mt][hh] = *reinterpret_cast<const u32x4*>(
+        stage + a_lds_offset(wm * 64 + mt * 32 + frag_row(lane), 4 * s + 2 * (lane >> 5) + hh));
+  } else {
+    const int q = u - 4;
+    f.b[s][q] = tr8_read(stage + A_STAGE_BYTES + btr8_offset(btr8_k(s, q, lane), btr8_n(nw, lane)));
+  }
+}
+
+// MFMA i (0..3) of an fp8 k-tile: k-step i / 2, m-subtile i % 2
+// (v_mfma_f32_32x32x64_f8f6f4, both operands e4m3, no block scales).
+__device__ inline void mma_piece8(const KTileFrags8& f, int i, f32x16 (&acc)[2][1]) {
+  const int s = i >> 1, mt = i & 1;
+  const u32x4 a0 = f.a[s][mt][0], a1 = f.a[s][mt][1];
+  const u32x2 b0 = f.b[s][0], b1 = f.b[s][1], b2 = f.b[s][2], b3 = f.b[s][3];
+  const i32x8 av = {(int)a0[0], (int)a0[1], (int)a0[2], (int)a0[3],
+                    (int)a1[0], (int)a1[1], (int)a1[2], (int)a1[3]};
+  const i32x8 bv = {(int)b0[0], (int)b0[1], (int)b1[0], (int)b1[1],
+                    (int)b2[0], (int)b2[1], (int)b3[0], (int)b3[1]};
+  acc[mt][0] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bv, av, acc[mt][0], 0, 0, 0, 0, 0, 0);
+}
+
 // 64-bit relaxed atomic access at agent scope for the row statistics.
 __device__ inline void store_stat(float2* p, float m, float s) {
   const uint64_t u = (uint64_t)__builtin_bit_cast(uint32_t, m) |
@@ -482,12 +526,27 @@ chain_tile_kernel(const ChainParams p) {
     // k-tile read zeros into stages that are never used.
     constexpr int S = C::kStages;
     constexpr int NB = C::kBlocksPerWave;
-    constexpr int LPT = 2 * NB;            // loads per wave per k-tile
-    constexpr int RPT = 4 * (2 + 2 * NTN);  // fragment reads per wave per k-tile
-    constexpr int MPT = 4 * 2 * NTN;        // MFMAs per wave per k-tile
+    constexpr bool F8 = IN_DT == DT_FP8;
+    constexpr int LPT = 2 * NB;                  // loads per wave per k-tile
+    constexpr int RPT = F8 ? 16 : 4 * (2 + 2 * NTN);  // fragment reads per wave per k-tile
+    constexpr int MPT = F8 ? 4 : 4 * 2 * NTN;         // MFMAs per wave per k-tile
+    static_assert(!F8 || NTN == 1, "fp8 fragments are laid out for 64x32 waves");
+    using Frags = std::conditional_t<F8, KTileFrags8, KTileFrags<NTN>>;
+    auto read_piece = [&](const uint8_t* st, int i, Frags& f) {
+      if constexpr (F8)
+        read_frag_piece8(st, lane, wm, nw, i, f);
+      else
+        read_frag_piece(st, lane, wm, nw, i, f);
+    };
+    auto mma = [&](const Frags& f, int i) {
+      if constexpr (F8)
+        mma_piece8(f, i, acc);
+      else
+        mma_piece<IN_DT>(f, i, acc);
+    };
     static_assert(RPT % LPT == 0 && MPT % LPT == 0, "k-tile step groups");
     const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-    DmaPlan<NB> d;
+    DmaPlan<IN_DT, NB> d;
     d.init(p.a + bt * p.a_bstride, p.b + bt * p.b_bstride, (uint32_t)p.a_bstride,
            (uint32_t)p.b_bstride, (uint32_t)row0, (uint32_t)n0, (uint32_t)p.M, (uint32_t)p.N,
            (uint32_t)p.K, (uint32_t)p.lda_bytes, (uint32_t)p.ldb_bytes, wave_u, lane);
@@ -498,9 +557,9 @@ chain_tile_kernel(const ChainParams p) {
       for (int q = 0; q < S - 1; ++q) d.issue(lds0 + q * STAGE_BYTES, q);
       load_gen0();  // newer than the k-tile loads: only makes the waits below stricter
       wait_loads_barrier<LPT * (S - 2)>();  // k-tile 0 landed
-      KTileFrags<NTN> f0, f1;
+      Frags f0, f1;
 #pragma unroll
-      for (int i = 0; i < RPT; ++i) read_frag_piece(smem, lane, wm, nw, i, f0);
+      for (int i = 0; i < RPT; ++i) read_piece(smem, i, f0);
       // One k-tile step, in LPT groups of (1 load of k-tile kt+S-1, RPT/LPT
       // fragment reads of k-tile kt+1, MPT/LPT MFMAs of k-tile kt).  A wave
       // that issues a direct-to-LDS load stalls until the memory pipeline
@@ -508,7 +567,7 @@ chain_tile_kernel(const ChainParams p) {
       // core busy through those stalls.  sched_barrier pins the groups (MFMAs
       // touch no memory, so the compiler would otherwise move them freely,
       // also across s_barrier).
-      auto step = [&](int kt, const KTileFrags<NTN>& cur, KTileFrags<NTN>& next) {
+      auto step = [&](int kt, const Frags& cur, Frags& next) {
         __builtin_amdgcn_sched_barrier(0);
         wait_loads_barrier<LPT * (S - 3)>();  // k-tile kt+1 landed; stage (kt-1)%S free
         __builtin_amdgcn_sched_barrier(0);
@@ -518,10 +577,9 @@ chain_tile_kernel(const ChainParams p) {
         for (int g = 0; g < LPT; ++g) {
           d.issue_one(fill, kt + S - 1, g);
 #pragma unroll
-          for (int i = 0; i < RPT / LPT; ++i)
-            read_frag_piece(rd, lane, wm, nw, (RPT / LPT) * g + i, next);
+          for (int i = 0; i < RPT / LPT; ++i) read_piece(rd, (RPT / LPT) * g + i, next);
 #pragma unroll
-          for (int i = 0; i < MPT / LPT; ++i) mma_piece<IN_DT>(cur, (MPT / LPT) * g + i, acc);
+          for (int i = 0; i < MPT / LPT; ++i) mma(cur, (MPT / LPT) * g + i);
           __builtin_amdgcn_sched_barrier(0);
         }
       };

@@ -143,6 +143,32 @@ WTC_HD constexpr int btr_k(int s, int h, int lane) {
 }
 WTC_HD constexpr int btr_n(int nb, int lane) { return nb + 16 * ((lane >> 4) & 1) + 4 * (lane & 3); }
 
+// ---- direct-to-LDS staging of 8-bit (fp8) k-tiles ---------------------------
+// A uses the 16-bit layout above unchanged (a chunk is 16 fp8 instead of 8
+// f16).  B stays K-major ([k][n], 128 bytes per k-row for BN = 128 columns,
+// 128 k-rows per k-tile) with 16-byte chunks XOR-swizzled by 2*((k/2)%4):
+// element (k, n) lives at btr8_offset(k, n).  B block b = k-rows 8b..8b+7;
+// lane i lands in row 8b + i/8, slot i%8, which holds chunk slot ^ 2*((row/2)%4).
+WTC_HD constexpr int btr8_offset(int k, int n) {
+  return k * 128 + ((((n >> 4) ^ (((k >> 1) & 3) << 1)) & 7) << 4) + (n & 15);
+}
+WTC_HD constexpr int dma8_b_row(int b, int lane) { return 8 * b + (lane >> 3); }
+WTC_HD constexpr int dma8_b_chunk(int b, int lane) {
+  return (lane & 7) ^ (((dma8_b_row(b, lane) >> 1) & 3) << 1);
+}
+// The fp8 MFMA (32x32x64) takes 32 bytes per lane: lane l supplies row /
+// column l%32 and, for k-step s, k = 64s + 32(l/32) + 0..31.  A arrives as
+// two ds_read_b128 of chunks 4s + 2(l/32) and 4s + 2(l/32) + 1.  B arrives
+// as four ds_read_b64_tr_b8 (q = 0..3); within each group of 16 lanes that
+// read returns to lane i, byte r, byte i%8 of the 8 bytes read by lane
+// 2r + i/8.  So source lane j of a group reads k-row 64s + 32h + 8q + j/2,
+// columns nb + 16*(group%2) + 8*(j%2) .. +7, and lane i of the group then
+// holds column nb + 16*(group%2) + i, k = 64s + 32h + 8q + r.
+WTC_HD constexpr int btr8_k(int s, int q, int lane) {
+  return 64 * s + 32 * (lane >> 5) + 8 * q + ((lane & 15) >> 1);
+}
+WTC_HD constexpr int btr8_n(int nb, int lane) { return nb + 16 * ((lane >> 4) & 1) + 8 * (lane & 1); }
+
 // ---- workgroup -> tile ------------------------------------------------------
 // Workgroups are dispatched round-robin over the 8 XCDs (blockIdx % 8).
 // tile_of_block() first gives XCD x the contiguous range of logical ids

@@ -20,13 +20,15 @@
 
 namespace wtc {
 
-// The kernel library's variants: a 128x128 output tile per 256-thread
-// workgroup, one 128-byte k-tile per pipeline step, 64x64 per wave, which
-// leaves each lane 2 output rows x 32 columns of accumulators.
+// The kernel library's variants: a 128x128 output tile per workgroup, one
+// 128-byte k-tile per pipeline step.  16-bit and fp8 inputs run 8 waves of
+// 64x32 (each lane: 2 output rows x 16 columns of accumulators), f32 runs 4
+// waves of 64x64 (2 rows x 32 columns).
 std::vector<Variant> supported_variants(Elem in) {
   const int64_t tk = elem_bytes(in) ? 128 / elem_bytes(in) : 0;
   if (tk == 0) return {};
-  return {Variant{TileParams{128, 128, tk, 2, 32}, "tile128x128_wave64x64"}};
+  if (in == Elem::F32) return {Variant{TileParams{128, 128, tk, 2, 32}, "tile128x128_wave64x64"}};
+  return {Variant{TileParams{128, 128, tk, 2, 16}, "tile128x128_wave64x32"}};
 }
 
 bool is_supported(const TileParams& t, Elem in) {
