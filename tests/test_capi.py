@@ -260,3 +260,16 @@ def test_reference_chain_files(L, tmp_path, fname, expect):
         m, n, k, dt = expect
         assert (launch["problem"]["m"], launch["problem"]["n"], launch["problem"]["k"]) == (m, n, k)
         assert launch["in_dtype"] == dt
+
+
+def test_one_hip_runtime_whichever_loads_first():
+    """Loading the library before torch must not map a second HIP runtime."""
+    import subprocess
+    import sys
+    code = ("from welder_typical_chain_amd import _lib; _lib.lib(); import torch, os; "
+            "m = open(f'/proc/{os.getpid()}/maps').read().splitlines(); "
+            "print(len({l.split()[-1] for l in m if 'libamdhip64' in l}))")
+    out = subprocess.run([sys.executable, "-c", code], cwd=str(PKG.parent), capture_output=True,
+                         text=True, timeout=300)
+    assert out.returncode == 0, out.stderr
+    assert out.stdout.strip() == "1"

@@ -80,6 +80,12 @@ def lib() -> ctypes.CDLL:
             raise RuntimeError(
                 f"{LIB_PATH} is missing: the HIP extension is not built "
                 "(run python -m welder_typical_chain_amd.build); no fallback exists")
+        # PyTorch ships its own HIP runtime (torch/lib/libamdhip64.so, soname
+        # libamdhip64.so.7) and asks for it as "libamdhip64.so".  Loaded first,
+        # it satisfies this library's libamdhip64.so.7 dependency, so one
+        # runtime serves both.  Loaded the other way round, the process would
+        # hold two HIP runtimes and the second one finds no device.
+        import torch  # noqa: F401
         h = ctypes.CDLL(str(LIB_PATH))
         for name, (res, args) in SIGNATURES.items():
             fn = getattr(h, name, None)
