@@ -53,6 +53,9 @@ HIP_FLAGS = [
     f"-I{ROOT / 'include'}",
     f"-I{CSRC}",
 ]
+# Per-source extra flags.  The chain tile kernel takes its first-load scalars
+# as leading arguments; gfx950 preloads those into SGPRs.
+HIP_EXTRA = {"fused_matmul_softmax.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"]}
 CXX_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra",
              f"-I{ROOT / 'include'}", f"-I{CSRC}"]
 
@@ -69,7 +72,7 @@ def _compile_one(src: str) -> Path:
     path = CSRC / src
     obj = OBJ / (src + ".o")
     if path.suffix == ".hip":
-        _run([HIPCC, *HIP_FLAGS, "-c", str(path), "-o", str(obj)])
+        _run([HIPCC, *HIP_FLAGS, *HIP_EXTRA.get(src, []), "-c", str(path), "-o", str(obj)])
     else:
         _run(["g++", *CXX_FLAGS, "-c", str(path), "-o", str(obj)])
     return obj
@@ -79,7 +82,7 @@ def _code_object(src: str) -> Path:
     """Device code object of one HIP source (same flags as the library)."""
     bundle = OBJ / (src + ".bundle")
     co = PKG / (Path(src).stem + f".{ARCH}.co")
-    _run([HIPCC, *HIP_FLAGS, "--genco", str(CSRC / src), "-o", str(bundle)])
+    _run([HIPCC, *HIP_FLAGS, *HIP_EXTRA.get(src, []), "--genco", str(CSRC / src), "-o", str(bundle)])
     _run([str(LLVM_BIN / "clang-offload-bundler"), "--unbundle", "--type=o",
           f"--targets=hipv4-amdgcn-amd-amdhsa--{ARCH}", f"--input={bundle}", f"--output={co}"])
     return co

@@ -465,9 +465,19 @@ __device__ inline void rowblock_barrier(uint32_t* sync, uint32_t g0, int nT, uin
 // -------------------------------------------------------------------------
 // The kernel
 // -------------------------------------------------------------------------
+// The leading scalar arguments are what a tile needs before its first load
+// is issued.  As separate kernel arguments they are preloaded into SGPRs on
+// gfx950 (this file is compiled with -amdgpu-kernarg-preload-count), so the
+// first k-tiles are requested without waiting for a kernarg fetch; the
+// ChainParams fields are only read after that.  grid32 is the launch's
+// workgroup count (gridDim.x would be read from the hidden kernel arguments
+// in memory).  Sizes and per-batch strides are 32-bit: the launcher keeps one
+// batch slice of A, B and out below 2 GiB.
 template <int IN_DT, int OUT_DT, int EPI, int PF>
 __global__ void __launch_bounds__(Cfg<IN_DT>::kThreads, 1)
-chain_tile_kernel(const ChainParams p) {
+chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32_t N32,
+                  uint32_t K32, uint32_t lda32, uint32_t ldb32, uint32_t nT32, uint32_t nRB32,
+                  uint32_t a_bs32, uint32_t b_bs32, uint32_t grid32, const ChainParams p) {
   using C = Cfg<IN_DT>;
   using L = EpiLayout<IN_DT, OUT_DT>;
   constexpr int NT = C::kThreads;
@@ -484,15 +494,14 @@ chain_tile_kernel(const ChainParams p) {
   const int nw = wn * 32 * NTN;  // first column of the wave's block
 
   uint32_t rbg, nt;  // row block across batches, column tile
-  tile_of_block(blockIdx.x, gridDim.x, gridDim.x / (uint32_t)p.nT, (uint32_t)p.nT, &rbg, &nt);
-  const uint32_t bt = rbg / (uint32_t)p.nRB;
-  const uint32_t rb = rbg - bt * (uint32_t)p.nRB;
+  tile_of_block(blockIdx.x, grid32, grid32 / nT32, nT32, &rbg, &nt);
+  const uint32_t bt = rbg / nRB32;
+  const uint32_t rb = rbg - bt * nRB32;
   const int64_t row0 = rb * BM;
   const int64_t n0 = nt * BN;
 
   constexpr int SZ = dtype_bytes(IN_DT);
-  uint8_t* o_base = p.out + bt * p.o_bstride;
-  const int nk = (int)((p.K * SZ + kKTileBytes - 1) / kKTileBytes);
+  const int nk = (int)(((uint64_t)K32 * SZ + kKTileBytes - 1) / kKTileBytes);
   // The row block's generation word, as it is before this tile arrives (it
   // cannot move until this tile has arrived).  Read by every lane,
   // unconditionally, once the first k-tiles are requested: the load then
@@ -547,9 +556,8 @@ chain_tile_kernel(const ChainParams p) {
     static_assert(RPT % LPT == 0 && MPT % LPT == 0, "k-tile step groups");
     const int wave_u = __builtin_amdgcn_readfirstlane(wave);
     DmaPlan<IN_DT, NB> d;
-    d.init(p.a + bt * p.a_bstride, p.b + bt * p.b_bstride, (uint32_t)p.a_bstride,
-           (uint32_t)p.b_bstride, (uint32_t)row0, (uint32_t)n0, (uint32_t)p.M, (uint32_t)p.N,
-           (uint32_t)p.K, (uint32_t)p.lda_bytes, (uint32_t)p.ldb_bytes, wave_u, lane);
+    d.init(a_in + (uint64_t)bt * a_bs32, b_in + (uint64_t)bt * b_bs32, a_bs32, b_bs32,
+           (uint32_t)row0, (uint32_t)n0, M32, N32, K32, lda32, ldb32, wave_u, lane);
     const uint32_t lds0 = (uint32_t)(uintptr_t)(WTC_LDS uint8_t*)smem;
     if (nk == 0) load_gen0();
     if (nk > 0) {
@@ -601,15 +609,15 @@ chain_tile_kernel(const ChainParams p) {
     // stays exact; the last nk % PF k-tiles run in a guarded tail.
     static_assert(NT == 256 && NTN == 2, "register path layout");
     Tile tl;
-    tl.ra = make_rsrc(p.a + bt * p.a_bstride, (uint32_t)p.a_bstride);
-    tl.rb = make_rsrc(p.b + bt * p.b_bstride, (uint32_t)p.b_bstride);
+    tl.ra = make_rsrc(a_in + (uint64_t)bt * a_bs32, a_bs32);
+    tl.rb = make_rsrc(b_in + (uint64_t)bt * b_bs32, b_bs32);
     tl.row0 = row0;
     tl.n0 = n0;
-    tl.M = p.M;
-    tl.N = p.N;
-    tl.K = p.K;
-    tl.lda = p.lda_bytes;
-    tl.ldb = p.ldb_bytes;
+    tl.M = M32;
+    tl.N = N32;
+    tl.K = K32;
+    tl.lda = lda32;
+    tl.ldb = ldb32;
     StageRegs<IN_DT> R[PF];
 #pragma unroll
     for (int q = 0; q < PF; ++q) R[q].load(tl, q, t);
@@ -791,6 +799,7 @@ chain_tile_kernel(const ChainParams p) {
   __syncthreads();
 
   // ---- scale, convert and store: 16 output bytes per thread per step -------
+  uint8_t* o_base = p.out + bt * p.o_bstride;
   constexpr int OSZ = OutTraits<OUT_DT>::SZ;
   constexpr int EPC = 16 / OSZ;       // elements per 16-byte chunk
   constexpr int CPR = BN / EPC;       // chunks per tile row

@@ -212,6 +212,24 @@ int launch_chain(const void* kern, int threads, int64_t grid, int lds_dyn,
   return WTC_OK;
 }
 
+// chain_tile_kernel: the scalars a tile needs before its first load lead the
+// argument list (preloaded into SGPRs), then the parameter block.  check_args
+// keeps every batch slice below 2 GiB, so the 32-bit sizes and strides hold.
+int launch_tile(const void* kern, int threads, int64_t grid, int lds_dyn,
+                const ChainParams& prm, hipStream_t stream) {
+  ChainParams p = prm;
+  const uint8_t* a = p.a;
+  const uint8_t* b = p.b;
+  uint32_t M = (uint32_t)p.M, N = (uint32_t)p.N, K = (uint32_t)p.K;
+  uint32_t lda = (uint32_t)p.lda_bytes, ldb = (uint32_t)p.ldb_bytes;
+  uint32_t nT = (uint32_t)p.nT, nRB = (uint32_t)p.nRB;
+  uint32_t a_bs = (uint32_t)p.a_bstride, b_bs = (uint32_t)p.b_bstride;
+  uint32_t g = (uint32_t)grid;
+  void* args[] = {&a, &b, &M, &N, &K, &lda, &ldb, &nT, &nRB, &a_bs, &b_bs, &g, &p};
+  HIP_TRY(hipLaunchKernel(kern, dim3((unsigned)grid), dim3(threads), args, (size_t)lds_dyn, stream));
+  return WTC_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -335,12 +353,12 @@ int wtc_matmul_softmax(const void* a, const void* b, void* out, int64_t batch, i
                         p, stream);
   }
   if (chosen == WTC_PATH_EXCHANGE) {
-    return launch_chain(chain_kernel_symbol(in_dtype, out_dtype, kEpiExchange),
+    return launch_tile(chain_kernel_symbol(in_dtype, out_dtype, kEpiExchange),
                         chain_kernel_threads(in_dtype), grid,
                         exchange_lds_pad(in_dtype, out_dtype), p, stream);
   }
   if (chosen == WTC_PATH_SPLIT) {
-    rc = launch_chain(chain_kernel_symbol(in_dtype, out_dtype, kEpiSplit),
+    rc = launch_tile(chain_kernel_symbol(in_dtype, out_dtype, kEpiSplit),
                       chain_kernel_threads(in_dtype), grid, 0, p, stream);
     if (rc) return rc;
     uint8_t* o = p.out;
@@ -362,8 +380,8 @@ int wtc_matmul_softmax(const void* a, const void* b, void* out, int64_t batch, i
   q.out = reinterpret_cast<uint8_t*>(logits);
   q.o_bstride = m * n * 4;
   q.ldo_bytes = n * 4;
-  rc = launch_chain(chain_kernel_symbol(in_dtype, DT_F32, kEpiLogits),
-                    chain_kernel_threads(in_dtype), grid, 0, q, stream);
+  rc = launch_tile(chain_kernel_symbol(in_dtype, DT_F32, kEpiLogits),
+                   chain_kernel_threads(in_dtype), grid, 0, q, stream);
   if (rc) return rc;
   const int64_t rows = batch * m;
   if (rows > 0x7FFFFFFFll) return fail(WTC_ERR_UNSUPPORTED, "too many rows");
