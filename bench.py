@@ -35,7 +35,9 @@ def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=500,
+                    help="untimed steps first (500 C2 steps, ~10 ms, bring the clocks to their "
+                         "steady state; a 10-step warmup times the first loop 2-5 %% slow)")
     ap.add_argument("--path", default="auto", choices=["auto", "exchange", "split", "unfused", "rows"])
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="budget of the cpu_baseline sample (0 disables it)")
