@@ -10,10 +10,10 @@
 //           merged across the 4 column-waves through LDS at the end;
 //   pass 2: the same products again, out = exp2(y - max) / sum, stored once.
 // The output is written exactly once and nothing else goes to HBM (no
-// workspace).  The row block's A fragments stay in registers for both
-// passes; the B column tiles stream through a 4-stage LDS ring of
-// direct-to-LDS loads (the same K-major, XOR-swizzled B layout and
-// transpose reads as chain_tile_kernel).
+// workspace).  The row block's A goes to LDS once and its MFMA fragments stay
+// in registers for both passes; the B column tiles stream through a 4-stage
+// LDS ring of direct-to-LDS loads (the same K-major, XOR-swizzled B layout
+// and transpose reads as chain_tile_kernel).
 //
 // 8 waves, 2 x 4: wave (wm, wn) owns rows wm*64 .. +63 and columns
 // wn*32 .. +31 of each tile (two 32x32 MFMA subtiles), 2 waves per SIMD.
@@ -161,6 +161,18 @@ chain_rows_kernel(const ChainParams p) {
     float rm[2] = {-INFINITY, -INFINITY}, rs[2] = {0.0f, 0.0f};
     float gsub[2] = {0.0f, 0.0f};  // pass 2: row max + log2(row sum)
     f32x16 ACC[2][2];              // [tile parity][m-subtile]
+    // The row block's A fragments (both m-subtiles, all k-steps: 64 VGPRs)
+    // are read from LDS once and kept in registers for both passes.  The A
+    // loads were issued before the B prologue, so waiting until only the
+    // B prologue loads are outstanding means this wave's A is in LDS; the
+    // barrier extends that to every wave's share.
+    wait_loads_barrier<BPW * (S - 1)>();
+    u32x4 areg[2][KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      areg[0][s] = read_a(0, s);
+      areg[1][s] = read_a(1, s);
+    }
 
     // Pass-1 statistics of one tile (FULL: no column of the tile is past N).
     auto ep1 = [&](auto full_c, const f32x16 (&acc)[2], int j) {
@@ -263,9 +275,9 @@ chain_rows_kernel(const ChainParams p) {
         for (int v = 0; v < 16; ++v) ACC[P][mt][v] = 0.0f;
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
-        const u32x4 b = read_b(st, s), a0 = read_a(0, s), a1 = read_a(1, s);
-        ACC[P][0] = mfma16<IN_DT>(b, a0, ACC[P][0]);
-        ACC[P][1] = mfma16<IN_DT>(b, a1, ACC[P][1]);
+        const u32x4 b = read_b(st, s);
+        ACC[P][0] = mfma16<IN_DT>(b, areg[0][s], ACC[P][0]);
+        ACC[P][1] = mfma16<IN_DT>(b, areg[1][s], ACC[P][1]);
       }
       const int jp = (it - 1) % nT;
       if constexpr (EP == 1) ep1(std::true_type{}, ACC[P ^ 1], jp);
