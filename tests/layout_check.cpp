@@ -327,6 +327,54 @@ int main() {
   run(2, "f16/bf16");
   run(1, "fp8");
   run(4, "f32");
+  // The direct-to-LDS load plan keeps only block 0's offsets per lane and
+  // steps to block b from there: A rows +8 per block with the chunk
+  // recomputed as (lane % 8) ^ ((4b + lane / 16) % 8); B rows +4 (16-bit) or
+  // +8 (fp8) per block with a block-independent chunk.  Checked for all 32
+  // A blocks of a 256-row tile and the 16 B blocks.
+  for (int b = 0; b < 32; ++b)
+    for (int l = 0; l < 64; ++l) {
+      CHECK(dma_a_row(b, l) == dma_a_row(0, l) + 8 * b, "dma_a_row step (b %d lane %d)\n", b, l);
+      CHECK(dma_a_chunk(b, l) == ((l & 7) ^ ((4 * b + (l >> 4)) & 7)),
+            "dma_a_chunk recomputation (b %d lane %d)\n", b, l);
+      CHECK(dma_a_chunk(b, l) == (dma_a_chunk(b & ~1, l) ^ ((b & 1) ? 4 : 0)),
+            "dma_a_chunk from the even block (b %d lane %d)\n", b, l);
+      if (b < 16) {
+        CHECK(dma_b_row(b, l) == dma_b_row(0, l) + 4 * b, "dma_b_row step (b %d lane %d)\n", b, l);
+        CHECK(dma_b_chunk(b, l) == dma_b_chunk(0, l), "dma_b_chunk depends on the block\n");
+        CHECK(dma8_b_row(b, l) == dma8_b_row(0, l) + 8 * b, "dma8_b_row step (b %d lane %d)\n", b, l);
+        CHECK(dma8_b_chunk(b, l) == dma8_b_chunk(0, l), "dma8_b_chunk depends on the block\n");
+      }
+    }
+  // Fragment reads as a per-lane base plus a compile-time offset (the kernel
+  // keeps only the bases): A m-subtile mt adds 4096 bytes; 16-bit B k-step s,
+  // half h add (16s + 4h) k-rows of 256 bytes; fp8 B k-step s, quad q add
+  // (64s + 8q) k-rows of 128 bytes.  For every lane and wave position.
+  for (int l = 0; l < 64; ++l)
+    for (int wm = 0; wm < 4; ++wm)
+      for (int mt = 0; mt < 2; ++mt)
+        for (int s = 0; s < 4; ++s) {
+          const int r = frag_row(l);
+          CHECK(a_lds_offset(wm * 64 + mt * 32 + r, frag_chunk(l, s)) ==
+                    a_lds_offset(wm * 64 + r, frag_chunk(l, s)) + mt * 4096,
+                "A fragment offset not base + 4096*mt (lane %d)\n", l);
+          const int c8 = 4 * (s >> 1) + 2 * (l >> 5) + (s & 1);
+          CHECK(a_lds_offset(wm * 64 + mt * 32 + r, c8) == a_lds_offset(wm * 64 + r, c8) + mt * 4096,
+                "fp8 A fragment offset not base + 4096*mt (lane %d)\n", l);
+        }
+  for (int l = 0; l < 64; ++l)
+    for (int nw = 0; nw < 128; nw += 32)
+      for (int s = 0; s < 4; ++s)
+        for (int h = 0; h < 4; ++h) {
+          if (h < 2)
+            CHECK(btr_offset(btr_k(s, h, l), btr_n(nw, l)) ==
+                      btr_offset(btr_k(0, 0, l), btr_n(nw, l)) + (16 * s + 4 * h) * 256,
+                  "B fragment offset not base + k-rows (lane %d s %d h %d)\n", l, s, h);
+          if (s < 2)
+            CHECK(btr8_offset(btr8_k(s, h, l), btr8_n(nw, l)) ==
+                      btr8_offset(btr8_k(0, 0, l), btr8_n(nw, l)) + (64 * s + 8 * h) * 128,
+                  "fp8 B fragment offset not base + k-rows (lane %d s %d q %d)\n", l, s, h);
+        }
   // tile_of_block: every (row block, column tile) exactly once
   for (auto rc : std::vector<std::pair<uint32_t, uint32_t>>{{16, 16}, {8, 256}, {1024, 16}, {2, 3}, {5, 7}, {3, 1}}) {
     const uint32_t R = rc.first, C = rc.second, G = R * C;

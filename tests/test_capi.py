@@ -71,15 +71,24 @@ def test_plan_headline_and_configs(L):
     rc, grid, path, _ = plan(L, 64, 2048, 2048, 128, 1, 1, _lib.PATH_AUTO)
     assert (rc, grid, path) == (0, 64 * 16, _lib.PATH_ROWS)
     rc, grid, path, _ = plan(L, 64, 2048, 2048, 128, 1, 1, _lib.PATH_SPLIT)
-    assert (rc, grid, path) == (0, 64 * 256, _lib.PATH_SPLIT)
+    assert (rc, grid, path) == (0, 64 * 8 * 16, _lib.PATH_SPLIT)  # 256-row tiles
     # the rows path needs 16-bit inputs and k <= 128
     assert plan(L, 64, 2048, 2048, 256, 1, 1, _lib.PATH_AUTO)[2] == _lib.PATH_SPLIT
     assert plan(L, 64, 2048, 2048, 128, _lib.DTYPE_FP8_E4M3, 1, _lib.PATH_AUTO)[2] == _lib.PATH_SPLIT
     rc, *_ = plan(L, 1, 256, 256, 256, 1, 1, _lib.PATH_ROWS)
     assert rc == _lib.WTC_ERR_UNSUPPORTED and b"rows path" in L.wtc_last_error()
-    # C4: 8 x 256 tiles, 256 column tiles per row -> split
+    # C4: 256 column tiles per row -> split, with 256-row tiles (4 x 256)
     rc, grid, path, _ = plan(L, 1, 1024, 32768, 4096, _lib.DTYPE_BF16, 1, _lib.PATH_AUTO)
-    assert (rc, grid, path) == (0, 8 * 256, _lib.PATH_SPLIT)
+    assert (rc, grid, path) == (0, 4 * 256, _lib.PATH_SPLIT)
+    # C5 (fp8): 32 x 64 256-row tiles
+    assert plan(L, 1, 8192, 8192, 4096, _lib.DTYPE_FP8_E4M3, 1, _lib.PATH_AUTO)[:3] == \
+        (0, 32 * 64, _lib.PATH_SPLIT)
+    # 256-row tiles only for an even number of 128-row blocks and >= 2 tiles per
+    # CU, never for f32: otherwise 128-row tiles
+    assert plan(L, 1, 1152, 32768, 4096, _lib.DTYPE_BF16, 1, _lib.PATH_SPLIT)[1] == 9 * 256
+    assert plan(L, 1, 256, 32768, 64, _lib.DTYPE_BF16, 1, _lib.PATH_SPLIT)[1] == 2 * 256
+    assert plan(L, 1, 1024, 32768, 64, _lib.DTYPE_F32, 0, _lib.PATH_SPLIT)[1] == 8 * 256
+    assert plan(L, 64, 200, 1000, 72, _lib.DTYPE_F16, 1, _lib.PATH_SPLIT)[1] == 64 * 8
     # forcing the exchange path where it cannot be co-resident is refused
     rc, *_ = plan(L, 1, 1024, 32768, 4096, _lib.DTYPE_BF16, 1, _lib.PATH_EXCHANGE)
     assert rc == _lib.WTC_ERR_UNSUPPORTED and b"co-resident" in L.wtc_last_error()

@@ -19,9 +19,11 @@
 
 namespace wtc {
 
-// Workgroup sizes of the kernels (defined with the kernels in the library).
+// Workgroup sizes of the kernels and the split path's tile height (defined
+// with the kernels and the launcher in the library).
 int chain_kernel_threads(int in_dt);
 int rows_kernel_threads();
+int split_tile_rows(int in_dt, int64_t batch, int64_t m, int64_t n, int cu_count);
 
 static std::string library_path() {
   Dl_info info{};
@@ -144,9 +146,10 @@ static int compile_impl(const char* input_mlir_path, const char* out_dir, int64_
     int lds;
     int block = 256;
   };
-  auto chain_sym = [](int in, int out, int epi) {
+  // chain_tile_kernel<in, out, epi, PF = 3, tile rows>
+  auto chain_sym = [](int in, int out, int epi, int tm = 128) {
     return "_ZN3wtc17chain_tile_kernelILi" + std::to_string(in) + "ELi" + std::to_string(out) +
-           "ELi" + std::to_string(epi) + "E";
+           "ELi" + std::to_string(epi) + "ELi3ELi" + std::to_string(tm) + "E";
   };
   const std::string out_t = "ILi" + std::to_string(out_code) + "E";
   std::vector<K> ks;
@@ -161,8 +164,9 @@ static int compile_impl(const char* input_mlir_path, const char* out_dir, int64_
     ks.push_back({"chain_tile_kernel<" + kin + "," + kout + ",exchange>",
                   chain_sym(in_code, out_code, 0), grid, 82944, tile_threads});
   } else if (path == WTC_PATH_SPLIT) {
-    ks.push_back({"chain_tile_kernel<" + kin + "," + kout + ",split>",
-                  chain_sym(in_code, out_code, 1), grid, 0, tile_threads});
+    const int tm = split_tile_rows(in_code, spec.batch, spec.m, spec.n, 256);
+    ks.push_back({"chain_tile_kernel<" + kin + "," + kout + ",split," + std::to_string(tm) + "x128>",
+                  chain_sym(in_code, out_code, 1, tm), grid, 0, tile_threads});
     ks.push_back({"rescale_rows_kernel<" + kout + ">", "_ZN3wtc19rescale_rows_kernel" + out_t,
                   (rows + 3) / 4, 8192});
   } else {

@@ -48,19 +48,31 @@ constexpr int BN = 128;
 constexpr int A_STAGE_BYTES = BM * kKTileBytes;                  // 16 KiB
 constexpr int STAGE_BYTES = A_STAGE_BYTES + BN * kKTileBytes;    // 32 KiB
 
-// Per input type: 16-bit and fp8 inputs stream through a 4-stage ring filled
-// by direct-to-LDS loads and run 8 waves (2 per SIMD: while one waits to
-// issue a load, the other issues MFMAs), each owning a 64x32 block; f32 goes
-// through a 2-stage ring filled from registers with 4 waves of 64x64.
-template <int IN_DT> struct Cfg {
+// Per input type and tile height TM: 16-bit and fp8 inputs stream through a
+// ring of direct-to-LDS loads and run 8 waves (2 per SIMD: while one waits to
+// issue a load, the other issues MFMAs), each owning 64 rows -- a 64x32 block
+// of a 128-row tile (4 stages of 32 KiB) or a 64x64 block of a 256-row tile
+// (3 stages of 48 KiB, for the split path of large problems: a quarter less
+// L2 and a third less LDS traffic per MFMA).  f32 goes through a 2-stage ring
+// filled from registers with 4 waves of 64x64 (TM = 128 only).  Every ring
+// keeps k-tiles kt+1 .. kt+3 in flight or landed while k-tile kt's fragments
+// are in registers, so 3 stages suffice when a stage may be refilled as soon
+// as its fragments have been read.
+template <int IN_DT, int TM = 128> struct Cfg {
   static constexpr bool kDma = IN_DT == DT_F16 || IN_DT == DT_BF16 || IN_DT == DT_FP8;
-  static constexpr int kWavesN = kDma ? 4 : 2;          // waves along N (2 along M)
-  static constexpr int kWaves = 2 * kWavesN;
+  static_assert(TM == 128 || (TM == 256 && kDma), "tile height");
+  static constexpr int kBM = TM;
+  static constexpr int kWavesM = kDma ? TM / 64 : 2;     // waves along M
+  static constexpr int kWavesN = kDma ? 8 / kWavesM : 2;  // waves along N
+  static constexpr int kWaves = kWavesM * kWavesN;
   static constexpr int kThreads = 64 * kWaves;
   static constexpr int kNT = BN / kWavesN / 32;          // 32-column subtiles per wave
-  static constexpr int kBlocksPerWave = 16 / kWaves;     // 1 KiB load blocks per operand
-  static constexpr int kStages = kDma ? 4 : 2;
-  static constexpr int kRingBytes = kStages * STAGE_BYTES;
+  static constexpr int kABlocksPerWave = TM / 8 / kWaves;  // 1 KiB load blocks of A
+  static constexpr int kBBlocksPerWave = 16 / kWaves;      // ... and of B
+  static constexpr int kAStageBytes = TM * kKTileBytes;
+  static constexpr int kStageBytes = kAStageBytes + BN * kKTileBytes;
+  static constexpr int kStages = kDma ? (TM == 256 ? 3 : 4) : 2;
+  static constexpr int kRingBytes = kStages * kStageBytes;
 };
 
 
@@ -68,13 +80,14 @@ template <int IN_DT> struct Cfg {
 // 4-float pad spreads the 32 rows one wave writes at a time over all banks).
 constexpr int kStagePitch = BN + 4;
 
-template <int IN_DT, int OUT_DT> struct EpiLayout {
-  static constexpr int STAGING = BM * kStagePitch * 4;
-  static constexpr int RING = Cfg<IN_DT>::kRingBytes;
+template <int IN_DT, int OUT_DT, int TM = 128> struct EpiLayout {
+  static constexpr int STAGING = TM * kStagePitch * 4;
+  static constexpr int RING = Cfg<IN_DT, TM>::kRingBytes;
   static constexpr int UNION = STAGING > RING ? STAGING : RING;
   static constexpr int RED_OFF = (UNION + 255) / 256 * 256;
-  // wstat[kWavesN][BM] (float2), factor[kWavesN][BM] (float)
-  static constexpr int TOTAL = RED_OFF + 3 * Cfg<IN_DT>::kWavesN * BM * 4;
+  // wstat[kWavesN][TM] (float2), factor[kWavesN][TM] (float)
+  static constexpr int TOTAL = RED_OFF + 3 * Cfg<IN_DT, TM>::kWavesN * TM * 4;
+  static_assert(TOTAL <= 160 * 1024, "LDS");
 };
 
 // -------------------------------------------------------------------------
@@ -157,21 +170,32 @@ template <int IN_DT> struct StageRegs {
 // past M and k-rows past K fall outside the descriptors' ranges by
 // themselves; columns past N are parked at kOutOfRange, which stays out of
 // range for every k-tile (kt*b_step < 2^31).
-template <int IN_DT, int NB>  // 1 KiB blocks per operand per wave
+// NBA / NBB: 1 KiB blocks of A / B per wave per k-tile; ASTAGE: bytes of the
+// A part of a stage (B follows it).  The wave's blocks are consecutive
+// (dma_block), so per lane only the first block's offsets are kept: A block
+// j is 8 rows further down (its chunk swizzle recomputed from the row), B
+// block j KR k-rows further (its column and chunk do not depend on the
+// block).  Few registers: the 256-row tile needs every one it can get.
+template <int IN_DT, int NBA, int NBB, int ASTAGE>
 struct DmaPlan {
   static constexpr int SZ = dtype_bytes(IN_DT);
   static constexpr int KE = kKTileBytes / SZ;  // k-rows of B per k-tile
+  static constexpr int KR = SZ == 1 ? 8 : 4;   // k-rows of B per 1 KiB block
+  static constexpr int LPT = NBA + NBB;        // loads per wave per k-tile
   i32x4 ra, rb;
-  uint32_t a_base[NB], b_base[NB];
-  uint32_t a_chunk[NB];  // byte offset of the lane's A chunk inside a k-tile
-  uint32_t k_bytes;      // K * 2
-  uint32_t b_step;       // 64 * ldb: bytes of B per k-tile
-  uint32_t lds_a[NB], lds_b[NB];  // LDS byte offsets of the wave's blocks in a stage
+  uint32_t a_off;        // byte offset of the lane's A row in block 0 (chunk added per block)
+  uint32_t b_off;        // B byte offset of the lane in block 0, kOutOfRange past N
+  uint32_t k_bytes;      // K * element bytes
+  uint32_t lda8, b_blk;  // 8 * lda: A bytes per block; KR * ldb: B bytes per block
+  uint32_t b_step;       // KE * ldb: bytes of B per k-tile
+  uint32_t lds_a0, lds_b0;  // LDS byte offsets of the wave's first A / B block in a stage
+  uint32_t a_chunk0;        // A chunk byte offset of the lane in its even blocks
+  static_assert(NBA % 2 == 0, "the wave's first A block is even");
 
   // All extents and pitches fit in 31 bits (the launcher checks that one
   // batch slice of A and of B is below 2 GiB), so everything here is 32-bit.
   __device__ inline void init(const void* a, const void* b, uint32_t a_bytes, uint32_t b_bytes,
-                              uint32_t row0, uint32_t n0, uint32_t M, uint32_t N, uint32_t K,
+                              uint32_t row0, uint32_t n0, uint32_t M_, uint32_t N, uint32_t K,
                               uint32_t lda, uint32_t ldb, int wave_u, int lane) {
     const i32x4 ra_v = raw_rsrc(a, a_bytes), rb_v = raw_rsrc(b, b_bytes);
 #pragma unroll
@@ -179,40 +203,62 @@ struct DmaPlan {
       ra[i] = __builtin_amdgcn_readfirstlane(ra_v[i]);
       rb[i] = __builtin_amdgcn_readfirstlane(rb_v[i]);
     }
+    (void)M_;
     k_bytes = K * SZ;
     b_step = KE * ldb;
-#pragma unroll
-    for (int j = 0; j < NB; ++j) {
-      const int blk = dma_block(wave_u, j, NB);
-      const uint32_t row = row0 + (uint32_t)dma_a_row(blk, lane);
-      a_chunk[j] = (uint32_t)dma_a_chunk(blk, lane) * kChunkBytes;
-      a_base[j] = row < M ? row * lda + a_chunk[j] : kOutOfRange;
-      // a B chunk is 16 bytes: 8 columns of 16-bit data, 16 of fp8
-      const uint32_t krow = SZ == 1 ? (uint32_t)dma8_b_row(blk, lane) : (uint32_t)dma_b_row(blk, lane);
-      const uint32_t n = n0 + (SZ == 1 ? 16u * (uint32_t)dma8_b_chunk(blk, lane)
-                                       : 8u * (uint32_t)dma_b_chunk(blk, lane));
-      b_base[j] = n < N ? krow * ldb + n * SZ : kOutOfRange;
-      lds_a[j] = blk * 1024;
-      lds_b[j] = A_STAGE_BYTES + blk * 1024;
-    }
+    lda8 = 8 * lda;
+    b_blk = KR * ldb;
+    const int blk_a0 = dma_block(wave_u, 0, NBA);
+    const int blk_b0 = dma_block(wave_u, 0, NBB);
+    a_off = (row0 + (uint32_t)dma_a_row(blk_a0, lane)) * lda;
+    a_chunk0 = (uint32_t)dma_a_chunk(blk_a0, lane) * kChunkBytes;
+    // a B chunk is 16 bytes: 8 columns of 16-bit data, 16 of fp8
+    const uint32_t krow = SZ == 1 ? (uint32_t)dma8_b_row(blk_b0, lane) : (uint32_t)dma_b_row(blk_b0, lane);
+    const uint32_t n = n0 + (SZ == 1 ? 16u * (uint32_t)dma8_b_chunk(blk_b0, lane)
+                                     : 8u * (uint32_t)dma_b_chunk(blk_b0, lane));
+    b_off = n < N ? krow * ldb + n * SZ : kOutOfRange;
+    lds_a0 = blk_a0 * 1024;
+    lds_b0 = ASTAGE + blk_b0 * 1024;
   }
 
-  // Load j (0 .. 2*NB-1) of k-tile kt: A block j/2 for even j, B block j/2 for odd j.
+  __device__ inline void issue_a(uint32_t stage, int kt, int q) const {
+    // block blk_a0 + q: row a_row + 8q, chunk slot (lane % 8) ^ ((row >> 1) % 8)
+    // = (lane % 8) ^ ((4 * blk + lane / 16) % 8) (dma_a_chunk); lane / 16 < 4,
+    // so for an even first block this is the first block's slot ^ 4 (q odd)
+    const uint32_t chunk = a_chunk0 ^ ((q & 1) ? 4u * kChunkBytes : 0u);
+    // Rows past M need no test: their offsets lie beyond the batch slice the
+    // buffer descriptor covers, so they read zero (and a row's values only
+    // ever reach that row's own outputs, which are not stored past M).
+    const uint32_t ka = (uint32_t)kt * kKTileBytes;
+    dma16(ra, ka + chunk < k_bytes ? a_off + q * lda8 + chunk + ka : kOutOfRange,
+          stage + lds_a0 + q * 1024);
+  }
+  __device__ inline void issue_b(uint32_t stage, int kt, int q) const {
+    dma16(rb, b_off != kOutOfRange ? b_off + q * b_blk + (uint32_t)kt * b_step : kOutOfRange,
+          stage + lds_b0 + q * 1024);
+  }
+
+  // Load j (0 .. LPT-1) of k-tile kt: A and B blocks alternate while both
+  // last, the rest of the larger operand follows.
   __device__ inline void issue_one(uint32_t stage, int kt, int j) const {
-    const int q = j >> 1;
-    if (j & 1) {
-      dma16(rb, b_base[q] + (uint32_t)kt * b_step, stage + lds_b[q]);
+    constexpr int PAIRS = NBA < NBB ? NBA : NBB;
+    if (j < 2 * PAIRS) {
+      if (j & 1)
+        issue_b(stage, kt, j >> 1);
+      else
+        issue_a(stage, kt, j >> 1);
+    } else if (NBB > NBA) {
+      issue_b(stage, kt, j - PAIRS);
     } else {
-      const uint32_t ka = (uint32_t)kt * kKTileBytes;
-      dma16(ra, ka + a_chunk[q] < k_bytes ? a_base[q] + ka : kOutOfRange, stage + lds_a[q]);
+      issue_a(stage, kt, j - PAIRS);
     }
   }
 
-  // One k-tile (A and B, 2 x 16 KiB over all waves) into the stage at LDS
-  // byte address `stage`.
+  // One k-tile (A and B over all waves) into the stage at LDS byte address
+  // `stage`.
   __device__ inline void issue(uint32_t stage, int kt) const {
 #pragma unroll
-    for (int j = 0; j < 2 * NB; ++j) issue_one(stage, kt, j);
+    for (int j = 0; j < LPT; ++j) issue_one(stage, kt, j);
   }
 };
 
@@ -327,22 +373,44 @@ struct KTileFrags {
   u32x4 a[4][2], b[4][NTN];
 };
 
+// Per-lane LDS offsets of a wave's fragment reads inside a stage.  Every read
+// of a k-tile is one of these plus a compile-time offset -- the m-subtile adds
+// 32 rows (4096 bytes: the A swizzle depends on row/2 mod 8 only), the
+// k-step and half (quad) of B add whole k-rows (its swizzle depends on k mod
+// 4, fp8: k/2 mod 4 only) -- so a step's reads need these few address
+// registers instead of one per read.  A: per k-step s the chunk 2s + lane/32
+// (16-bit) or, for fp8, entry 2s + hh for chunk 4s + 2(lane/32) + hh.  B: per
+// n-subtile, k-step 0, half / quad 0.
+template <bool F8, int NTN, int ASTAGE>
+struct FragBase {
+  uint32_t a[4], b[NTN];
+  __device__ inline void init(int lane, int wm, int nw) {
+    const int r = frag_row(lane);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = F8 ? 4 * (i >> 1) + 2 * (lane >> 5) + (i & 1) : frag_chunk(lane, i);
+      a[i] = (uint32_t)a_lds_offset(wm * 64 + r, c);
+    }
+#pragma unroll
+    for (int nt = 0; nt < NTN; ++nt)
+      b[nt] = (uint32_t)(ASTAGE + (F8 ? btr8_offset(btr8_k(0, 0, lane), btr8_n(nw + nt * 32, lane))
+                                      : btr_offset(btr_k(0, 0, lane), btr_n(nw + nt * 32, lane))));
+  }
+};
+
 // LDS read i of a k-tile's fragments (2 + 2*NTN reads per k-step s): the two
 // A fragments (ds_read_b128), then the halves of the NTN B fragments
-// (ds_read_b64_tr_b16).  The wave's B columns start at nw.
-template <int NTN>
-__device__ inline void read_frag_piece(const uint8_t* stage, int lane, int wm, int nw, int i,
-                                       KTileFrags<NTN>& f) {
+// (ds_read_b64_tr_b16).
+template <int NTN, int ASTAGE>
+__device__ inline void read_frag_piece(const uint8_t* stage, const FragBase<false, NTN, ASTAGE>& fb,
+                                       int i, KTileFrags<NTN>& f) {
   constexpr int RPS = 2 + 2 * NTN;
   const int s = i / RPS, u = i % RPS;
-  const int r = frag_row(lane);
   if (u < 2) {
-    f.a[s][u] = *reinterpret_cast<const u32x4*>(
-        stage + a_lds_offset(wm * 64 + u * 32 + r, frag_chunk(lane, s)));
+    f.a[s][u] = *reinterpret_cast<const u32x4*>(stage + fb.a[s] + u * 4096);
   } else {
     const int nt = (u - 2) >> 1, h = (u - 2) & 1;
-    const u32x2 v = tr_read(stage + A_STAGE_BYTES +
-                            btr_offset(btr_k(s, h, lane), btr_n(nw + nt * 32, lane)));
+    const u32x2 v = tr_read(stage + fb.b[nt] + (16 * s + 4 * h) * 256);
     f.b[s][nt][2 * h] = v[0];
     f.b[s][nt][2 * h + 1] = v[1];
   }
@@ -363,40 +431,44 @@ __device__ inline void mma_piece(const KTileFrags<NTN>& f, int i, f32x16 (&acc)[
 }
 
 // fp8 (e4m3) operands of one k-tile (128 k = 2 MFMA k-steps of 64) for one
-// wave of 64 rows x 32 columns: A [step][m-subtile][16-byte half],
-// B [step][8-byte transpose read].
+// wave of 64 rows x 32*NTN columns: A [step][m-subtile][16-byte half],
+// B [step][n-subtile][8-byte transpose read].
+template <int NTN>
 struct KTileFrags8 {
   u32x4 a[2][2][2];
-  u32x2 b[2][4];
+  u32x2 b[2][NTN][4];
 };
 
-// LDS read i (0..15) of an fp8 k-tile's fragments: for k-step s = i / 8,
-// reads 0-3 are the A halves (ds_read_b128: chunks 4s + 2(lane/32) + 0/1
-// of m-subtiles 0, 1), reads 4-7 the four ds_read_b64_tr_b8 of B.
-__device__ inline void read_frag_piece8(const uint8_t* stage, int lane, int wm, int nw, int i,
-                                        KTileFrags8& f) {
-  const int s = i / 8, u = i % 8;
+// LDS read i (0 .. 2*(4+4*NTN)-1) of an fp8 k-tile's fragments: per k-step
+// s, reads 0-3 are the A halves (ds_read_b128: chunks 4s + 2(lane/32) + 0/1
+// of m-subtiles 0, 1), then four ds_read_b64_tr_b8 of B per n-subtile.
+template <int NTN, int ASTAGE>
+__device__ inline void read_frag_piece8(const uint8_t* stage, const FragBase<true, NTN, ASTAGE>& fb,
+                                        int i, KTileFrags8<NTN>& f) {
+  constexpr int RPS = 4 + 4 * NTN;
+  const int s = i / RPS, u = i % RPS;
   if (u < 4) {
     const int mt = u >> 1, hh = u & 1;
-    f.a[s][mt][hh] = *reinterpret_cast<const u32x4*>(
-        stage + a_lds_offset(wm * 64 + mt * 32 + frag_row(lane), 4 * s + 2 * (lane >> 5) + hh));
+    f.a[s][mt][hh] = *reinterpret_cast<const u32x4*>(stage + fb.a[2 * s + hh] + mt * 4096);
   } else {
-    const int q = u - 4;
-    f.b[s][q] = tr8_read(stage + A_STAGE_BYTES + btr8_offset(btr8_k(s, q, lane), btr8_n(nw, lane)));
+    const int nt = (u - 4) >> 2, q = (u - 4) & 3;
+    f.b[s][nt][q] = tr8_read(stage + fb.b[nt] + (64 * s + 8 * q) * 128);
   }
 }
 
-// MFMA i (0..3) of an fp8 k-tile: k-step i / 2, m-subtile i % 2
-// (v_mfma_f32_32x32x64_f8f6f4, both operands e4m3, no block scales).
-__device__ inline void mma_piece8(const KTileFrags8& f, int i, f32x16 (&acc)[2][1]) {
-  const int s = i >> 1, mt = i & 1;
+// MFMA i (0 .. 4*NTN-1) of an fp8 k-tile: k-step i / (2*NTN), m-subtile
+// (i / NTN) % 2, n-subtile i % NTN (v_mfma_f32_32x32x64_f8f6f4, both
+// operands e4m3, no block scales).
+template <int NTN>
+__device__ inline void mma_piece8(const KTileFrags8<NTN>& f, int i, f32x16 (&acc)[2][NTN]) {
+  const int s = i / (2 * NTN), mt = (i / NTN) & 1, nt = i % NTN;
   const u32x4 a0 = f.a[s][mt][0], a1 = f.a[s][mt][1];
-  const u32x2 b0 = f.b[s][0], b1 = f.b[s][1], b2 = f.b[s][2], b3 = f.b[s][3];
+  const u32x2 b0 = f.b[s][nt][0], b1 = f.b[s][nt][1], b2 = f.b[s][nt][2], b3 = f.b[s][nt][3];
   const i32x8 av = {(int)a0[0], (int)a0[1], (int)a0[2], (int)a0[3],
                     (int)a1[0], (int)a1[1], (int)a1[2], (int)a1[3]};
   const i32x8 bv = {(int)b0[0], (int)b0[1], (int)b1[0], (int)b1[1],
                     (int)b2[0], (int)b2[1], (int)b3[0], (int)b3[1]};
-  acc[mt][0] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bv, av, acc[mt][0], 0, 0, 0, 0, 0, 0);
+  acc[mt][nt] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bv, av, acc[mt][nt], 0, 0, 0, 0, 0, 0);
 }
 
 // 64-bit relaxed atomic access at agent scope for the row statistics.
@@ -462,6 +534,14 @@ __device__ inline void rowblock_barrier(uint32_t* sync, uint32_t g0, int nT, uin
   __hip_atomic_fetch_max(err + 1, w32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Groups of one main-loop step: the smallest g >= loads that divides both
+// the fragment reads and the MFMAs of a k-tile (0 if none does).
+constexpr int step_groups(int loads, int reads, int mfmas) {
+  for (int g = loads; g <= reads && g <= mfmas; ++g)
+    if (reads % g == 0 && mfmas % g == 0) return g;
+  return 0;
+}
+
 // -------------------------------------------------------------------------
 // The kernel
 // -------------------------------------------------------------------------
@@ -473,13 +553,15 @@ __device__ inline void rowblock_barrier(uint32_t* sync, uint32_t g0, int nT, uin
 // workgroup count (gridDim.x would be read from the hidden kernel arguments
 // in memory).  Sizes and per-batch strides are 32-bit: the launcher keeps one
 // batch slice of A, B and out below 2 GiB.
-template <int IN_DT, int OUT_DT, int EPI, int PF>
-__global__ void __launch_bounds__(Cfg<IN_DT>::kThreads, 1)
+template <int IN_DT, int OUT_DT, int EPI, int PF, int TM>
+__global__ void __launch_bounds__((Cfg<IN_DT, TM>::kThreads), 1)
 chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32_t N32,
                   uint32_t K32, uint32_t lda32, uint32_t ldb32, uint32_t nT32, uint32_t nRB32,
                   uint32_t a_bs32, uint32_t b_bs32, uint32_t grid32, const ChainParams p) {
-  using C = Cfg<IN_DT>;
-  using L = EpiLayout<IN_DT, OUT_DT>;
+  using C = Cfg<IN_DT, TM>;
+  using L = EpiLayout<IN_DT, OUT_DT, TM>;
+  static_assert(EPI != kEpiExchange || TM == 128, "the exchange path runs 128-row tiles");
+  constexpr int BM = TM;  // tile rows
   constexpr int NT = C::kThreads;
   constexpr int WN = C::kWavesN;
   constexpr int NTN = C::kNT;
@@ -525,69 +607,79 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
   if constexpr (C::kDma) {
-    // ---- main loop, 16-bit: 4-stage ring of direct-to-LDS loads -----------
+    // ---- main loop, 16-bit / fp8: ring of direct-to-LDS loads -------------
     // k-tile j goes to stage j % S.  Iteration kt: wait until k-tile kt+1 has
     // landed (its fragments are read during this iteration) and every wave
-    // is done with stage (kt-1) % S, refill that stage with k-tile kt+S-1,
+    // has read k-tile kt's fragments (last iteration), refill stage
+    // (kt+3) % S -- free by then for S = 3 and S = 4 -- with k-tile kt+3,
     // read k-tile kt+1's fragments into registers and run k-tile kt's MFMAs
-    // from the fragments read one iteration earlier -- the MFMAs never wait
-    // for LDS.  Each wave issues LPT loads per k-tile.  Loads past the last
-    // k-tile read zeros into stages that are never used.
+    // from the fragments read one iteration earlier: the MFMAs never wait
+    // for LDS, and k-tiles kt+2, kt+3 stay in flight.  Each wave issues LPT
+    // loads per k-tile.  Loads past the last k-tile read zeros into stages
+    // that are never used.
     constexpr int S = C::kStages;
-    constexpr int NB = C::kBlocksPerWave;
+    constexpr int D = 3;  // k-tiles requested ahead of the one whose MFMAs run
+    static_assert(S >= D, "ring depth");
+    constexpr int ASTAGE = C::kAStageBytes;
+    constexpr int STAGE = C::kStageBytes;
     constexpr bool F8 = IN_DT == DT_FP8;
-    constexpr int LPT = 2 * NB;                  // loads per wave per k-tile
-    constexpr int RPT = F8 ? 16 : 4 * (2 + 2 * NTN);  // fragment reads per wave per k-tile
-    constexpr int MPT = F8 ? 4 : 4 * 2 * NTN;         // MFMAs per wave per k-tile
-    static_assert(!F8 || NTN == 1, "fp8 fragments are laid out for 64x32 waves");
-    using Frags = std::conditional_t<F8, KTileFrags8, KTileFrags<NTN>>;
+    using Plan = DmaPlan<IN_DT, C::kABlocksPerWave, C::kBBlocksPerWave, ASTAGE>;
+    constexpr int LPT = Plan::LPT;                            // loads per wave per k-tile
+    constexpr int RPT = F8 ? 2 * (4 + 4 * NTN) : 4 * (2 + 2 * NTN);  // fragment reads
+    constexpr int MPT = F8 ? 4 * NTN : 4 * 2 * NTN;                  // MFMAs
+    // G groups per k-tile step: the fewest (>= LPT) that divide the reads
+    // and the MFMAs evenly
+    constexpr int G = step_groups(LPT, RPT, MPT);
+    static_assert(G > 0, "k-tile step groups");
+    using Frags = std::conditional_t<F8, KTileFrags8<NTN>, KTileFrags<NTN>>;
+    FragBase<F8, NTN, ASTAGE> fb;
+    fb.init(lane, wm, nw);
     auto read_piece = [&](const uint8_t* st, int i, Frags& f) {
       if constexpr (F8)
-        read_frag_piece8(st, lane, wm, nw, i, f);
+        read_frag_piece8<NTN, ASTAGE>(st, fb, i, f);
       else
-        read_frag_piece(st, lane, wm, nw, i, f);
+        read_frag_piece<NTN, ASTAGE>(st, fb, i, f);
     };
     auto mma = [&](const Frags& f, int i) {
       if constexpr (F8)
-        mma_piece8(f, i, acc);
+        mma_piece8<NTN>(f, i, acc);
       else
         mma_piece<IN_DT>(f, i, acc);
     };
-    static_assert(RPT % LPT == 0 && MPT % LPT == 0, "k-tile step groups");
     const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-    DmaPlan<IN_DT, NB> d;
+    Plan d;
     d.init(a_in + (uint64_t)bt * a_bs32, b_in + (uint64_t)bt * b_bs32, a_bs32, b_bs32,
            (uint32_t)row0, (uint32_t)n0, M32, N32, K32, lda32, ldb32, wave_u, lane);
     const uint32_t lds0 = (uint32_t)(uintptr_t)(WTC_LDS uint8_t*)smem;
     if (nk == 0) load_gen0();
     if (nk > 0) {
 #pragma unroll
-      for (int q = 0; q < S - 1; ++q) d.issue(lds0 + q * STAGE_BYTES, q);
+      for (int q = 0; q < D; ++q) d.issue(lds0 + q * STAGE, q);
       load_gen0();  // newer than the k-tile loads: only makes the waits below stricter
-      wait_loads_barrier<LPT * (S - 2)>();  // k-tile 0 landed
+      wait_loads_barrier<LPT * (D - 1)>();  // k-tile 0 landed
       Frags f0, f1;
 #pragma unroll
       for (int i = 0; i < RPT; ++i) read_piece(smem, i, f0);
-      // One k-tile step, in LPT groups of (1 load of k-tile kt+S-1, RPT/LPT
-      // fragment reads of k-tile kt+1, MPT/LPT MFMAs of k-tile kt).  A wave
-      // that issues a direct-to-LDS load stalls until the memory pipeline
-      // accepts it; spreading the MFMAs between the loads keeps the matrix
-      // core busy through those stalls.  sched_barrier pins the groups (MFMAs
-      // touch no memory, so the compiler would otherwise move them freely,
-      // also across s_barrier).
+      // One k-tile step, in G groups of (a load of k-tile kt+3 in the first
+      // LPT groups, RPT/G fragment reads of k-tile kt+1, MPT/G MFMAs of
+      // k-tile kt).  A wave that issues a direct-to-LDS load stalls until the
+      // memory pipeline accepts it; spreading the MFMAs between the loads
+      // keeps the matrix core busy through those stalls.  sched_barrier pins
+      // the groups (MFMAs touch no memory, so the compiler would otherwise
+      // move them freely, also across s_barrier).
       auto step = [&](int kt, const Frags& cur, Frags& next) {
         __builtin_amdgcn_sched_barrier(0);
-        wait_loads_barrier<LPT * (S - 3)>();  // k-tile kt+1 landed; stage (kt-1)%S free
+        wait_loads_barrier<LPT * (D - 2)>();  // k-tile kt+1 landed; kt's fragments read
         __builtin_amdgcn_sched_barrier(0);
-        const uint32_t fill = lds0 + ((kt + S - 1) % S) * STAGE_BYTES;
-        const uint8_t* rd = smem + ((kt + 1) % S) * STAGE_BYTES;
+        const uint32_t fill = lds0 + ((kt + D) % S) * STAGE;
+        const uint8_t* rd = smem + ((kt + 1) % S) * STAGE;
 #pragma unroll
-        for (int g = 0; g < LPT; ++g) {
-          d.issue_one(fill, kt + S - 1, g);
+        for (int g = 0; g < G; ++g) {
+          if (g < LPT) d.issue_one(fill, kt + D, g);
 #pragma unroll
-          for (int i = 0; i < RPT / LPT; ++i) read_piece(rd, (RPT / LPT) * g + i, next);
+          for (int i = 0; i < RPT / G; ++i) read_piece(rd, (RPT / G) * g + i, next);
 #pragma unroll
-          for (int i = 0; i < MPT / LPT; ++i) mma(cur, (MPT / LPT) * g + i);
+          for (int i = 0; i < MPT / G; ++i) mma(cur, (MPT / G) * g + i);
           __builtin_amdgcn_sched_barrier(0);
         }
       };
@@ -833,7 +925,7 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
 template <int OUT_DT>
 __global__ void __launch_bounds__(256)
 rescale_rows_kernel(uint8_t* __restrict__ out, const float2* __restrict__ partial,
-                    int64_t rows_total, int64_t M, int64_t nRB, int64_t N,
+                    int64_t rows_total, int64_t M, int64_t rows_pad, int64_t N,
                     int64_t ldo_bytes, int64_t o_bstride, int nT) {
   constexpr int ROWS_PER_WG = 4;
   constexpr int MAX_NT = 512;
@@ -845,8 +937,8 @@ rescale_rows_kernel(uint8_t* __restrict__ out, const float2* __restrict__ partia
   if (live) {
     bt = grow / M;
     m = grow % M;
-    const int64_t rbg = bt * nRB + m / BM;
-    const float2* st = partial + (rbg * BM + (m % BM)) * nT;  // [row][column tile]
+    // [batch][row, padded to the tile height: rows_pad per batch][column tile]
+    const float2* st = partial + (bt * rows_pad + m) * nT;
     float gm = -INFINITY;
     for (int q = lane; q < nT; q += 64) gm = fmaxf(gm, st[q].x);
 #pragma unroll
@@ -904,17 +996,17 @@ __global__ void zero_words_kernel(uint32_t* __restrict__ p, int64_t n) {
 // -------------------------------------------------------------------------
 constexpr int kPF = 3;
 
-template <int IN_DT, int OUT_DT, int EPI>
+template <int IN_DT, int OUT_DT, int EPI, int TM>
 static const void* tile_kernel_ptr() {
-  return reinterpret_cast<const void*>(&chain_tile_kernel<IN_DT, OUT_DT, EPI, kPF>);
+  return reinterpret_cast<const void*>(&chain_tile_kernel<IN_DT, OUT_DT, EPI, kPF, TM>);
 }
 
-template <int IN_DT, int EPI>
+template <int IN_DT, int EPI, int TM>
 static const void* by_out(int out_dt) {
   switch (out_dt) {
-    case DT_F32: return tile_kernel_ptr<IN_DT, DT_F32, EPI>();
-    case DT_F16: return tile_kernel_ptr<IN_DT, DT_F16, EPI>();
-    case DT_BF16: return tile_kernel_ptr<IN_DT, DT_BF16, EPI>();
+    case DT_F32: return tile_kernel_ptr<IN_DT, DT_F32, EPI, TM>();
+    case DT_F16: return tile_kernel_ptr<IN_DT, DT_F16, EPI, TM>();
+    case DT_BF16: return tile_kernel_ptr<IN_DT, DT_BF16, EPI, TM>();
   }
   return nullptr;
 }
@@ -922,15 +1014,27 @@ static const void* by_out(int out_dt) {
 template <int EPI>
 static const void* by_in(int in_dt, int out_dt) {
   switch (in_dt) {
-    case DT_F32: return by_out<DT_F32, EPI>(out_dt);
-    case DT_F16: return by_out<DT_F16, EPI>(out_dt);
-    case DT_BF16: return by_out<DT_BF16, EPI>(out_dt);
-    case DT_FP8: return by_out<DT_FP8, EPI>(out_dt);
+    case DT_F32: return by_out<DT_F32, EPI, 128>(out_dt);
+    case DT_F16: return by_out<DT_F16, EPI, 128>(out_dt);
+    case DT_BF16: return by_out<DT_BF16, EPI, 128>(out_dt);
+    case DT_FP8: return by_out<DT_FP8, EPI, 128>(out_dt);
   }
   return nullptr;
 }
 
-const void* chain_kernel_symbol(int in_dt, int out_dt, int epi) {
+// 256-row tiles: the split path with 16-bit or fp8 inputs.
+static const void* split256_by_in(int in_dt, int out_dt) {
+  switch (in_dt) {
+    case DT_F16: return by_out<DT_F16, kEpiSplit, 256>(out_dt);
+    case DT_BF16: return by_out<DT_BF16, kEpiSplit, 256>(out_dt);
+    case DT_FP8: return by_out<DT_FP8, kEpiSplit, 256>(out_dt);
+  }
+  return nullptr;
+}
+
+const void* chain_kernel_symbol(int in_dt, int out_dt, int epi, int tile_rows) {
+  if (tile_rows == 256) return epi == kEpiSplit ? split256_by_in(in_dt, out_dt) : nullptr;
+  if (tile_rows != 128) return nullptr;
   if (epi == kEpiExchange) return by_in<kEpiExchange>(in_dt, out_dt);
   if (epi == kEpiSplit) return by_in<kEpiSplit>(in_dt, out_dt);
   if (epi == kEpiLogits) return by_in<kEpiLogits>(in_dt, out_dt);

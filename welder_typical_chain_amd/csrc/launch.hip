@@ -13,6 +13,19 @@
 #include "wtc/wtc_hip.h"
 #include "wtc_kernels.h"
 
+// Tile height of the split path: 256-row tiles (a quarter less L2 and a
+// third less LDS traffic per MFMA) for 16-bit and fp8 inputs when they add
+// no padding rows (an even number of 128-row blocks) and the problem still
+// gives every CU at least two of them; 128 otherwise.
+namespace wtc {
+int split_tile_rows(int in_dt, int64_t batch, int64_t m, int64_t n, int cu_count) {
+  if (in_dt == DT_F32) return 128;
+  const int64_t rb128 = (m + 127) / 128;
+  const int64_t tiles256 = batch * (rb128 / 2) * ((n + 127) / 128);
+  return rb128 % 2 == 0 && tiles256 >= 2 * (int64_t)cu_count ? 256 : 128;
+}
+}  // namespace wtc
+
 namespace {
 
 using namespace wtc;
@@ -63,7 +76,8 @@ WsLayout ws_layout(int64_t batch, int64_t m, int64_t n, int path) {
   w.sync_off = 256;
   w.sync_bytes = kSyncRegion;
   w.partial_off = w.sync_off + w.sync_bytes;
-  w.partial_bytes = align256(rbs * kTile * nT * 8);
+  // statistics rows padded to 256 per batch (either tile height of the split path)
+  w.partial_bytes = align256(batch * ceil_div(m, 256) * 256 * nT * 8);
   w.total = w.partial_off + w.partial_bytes;
   if (path == WTC_PATH_UNFUSED) {
     w.logits_off = w.total;
@@ -123,7 +137,14 @@ int plan_impl(int64_t batch, int64_t m, int64_t n, int64_t k, int in_dt, int out
   if (p == WTC_PATH_SPLIT && ceil_div(n, kTile) > kRescaleMaxTiles)
     return fail(WTC_ERR_UNSUPPORTED, "split path supports n <= 65536");
   if (tiles > 0x7FFFFFFFll) return fail(WTC_ERR_UNSUPPORTED, "too many tiles for one grid");
-  if (grid) *grid = p == WTC_PATH_ROWS ? rbs : tiles;
+  if (grid) {
+    if (p == WTC_PATH_ROWS)
+      *grid = rbs;
+    else if (p == WTC_PATH_SPLIT)
+      *grid = batch * ceil_div(m, split_tile_rows(in_dt, batch, m, n, cu_count)) * nT;
+    else
+      *grid = tiles;
+  }
   if (chosen) *chosen = p;
   if (ws_bytes) *ws_bytes = ws_layout(batch, m, n, p).total;
   return WTC_OK;
@@ -341,7 +362,10 @@ int wtc_matmul_softmax(const void* a, const void* b, void* out, int64_t batch, i
   p.ldo_bytes = n * osz;
   p.c2 = lin * 1.4426950408889634f;
   p.lin_scale = lin;
-  p.nRB = (int)ceil_div(m, kTile);
+  // row blocks per batch of the tile kernel that runs
+  const int tile_rows =
+      chosen == WTC_PATH_SPLIT ? split_tile_rows(in_dtype, batch, m, n, ds->cu_count) : kTile;
+  p.nRB = (int)ceil_div(m, tile_rows);
   p.nT = (int)ceil_div(n, kTile);
   p.partial = reinterpret_cast<float2*>(wsb + L.partial_off);
   p.sync = reinterpret_cast<uint32_t*>(wsb + L.sync_off);
@@ -358,15 +382,16 @@ int wtc_matmul_softmax(const void* a, const void* b, void* out, int64_t batch, i
                         exchange_lds_pad(in_dtype, out_dtype), p, stream);
   }
   if (chosen == WTC_PATH_SPLIT) {
-    rc = launch_tile(chain_kernel_symbol(in_dtype, out_dtype, kEpiSplit),
+    rc = launch_tile(chain_kernel_symbol(in_dtype, out_dtype, kEpiSplit, tile_rows),
                       chain_kernel_threads(in_dtype), grid, 0, p, stream);
     if (rc) return rc;
     uint8_t* o = p.out;
     const float2* part = p.partial;
-    int64_t rows_total = batch * m, M_ = m, nRB = p.nRB, N_ = n, ldo = p.ldo_bytes,
-            ob = p.o_bstride;
+    // statistics rows per batch: the tile kernel's row blocks times its height
+    int64_t rows_total = batch * m, M_ = m, rows_pad = (int64_t)p.nRB * tile_rows, N_ = n,
+            ldo = p.ldo_bytes, ob = p.o_bstride;
     int nT = p.nT;
-    void* args[] = {&o, &part, &rows_total, &M_, &nRB, &N_, &ldo, &ob, &nT};
+    void* args[] = {&o, &part, &rows_total, &M_, &rows_pad, &N_, &ldo, &ob, &nT};
     HIP_TRY(hipLaunchKernel(rescale_kernel_symbol(out_dtype),
                             dim3((unsigned)ceil_div(rows_total, kRescaleRowsPerWg)), dim3(256),
                             args, 0, stream));

@@ -35,10 +35,14 @@ struct ChainParams {
   uint64_t spin_ticks;  // row-block wait limit, 100 MHz ticks
 };
 
-const void* chain_kernel_symbol(int in_dt, int out_dt, int epi);
+// tile_rows: 128, or 256 for the split path with 16-bit or fp8 inputs (else NULL).
+const void* chain_kernel_symbol(int in_dt, int out_dt, int epi, int tile_rows = 128);
 const void* rescale_kernel_symbol(int out_dt);
 const void* zero_kernel_symbol();
 int chain_kernel_lds_bytes(int in_dt, int out_dt);
+// Tile height (128 or 256) the split path uses for this problem on a device
+// with cu_count compute units.
+int split_tile_rows(int in_dt, int64_t batch, int64_t m, int64_t n, int cu_count);
 int chain_kernel_threads(int in_dt);  // workgroup size of chain_tile_kernel
 
 // One workgroup per 128-row block, two passes over N (K <= rows_kernel_max_k()).
