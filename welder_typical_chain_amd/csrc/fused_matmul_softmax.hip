@@ -6,15 +6,19 @@
 // (reference: bench/baselines/default/fused/04c.after_linalg_to_loops.mlir:41-313,
 // chain spec mlir/matmul_softmax_chain_f16_native.mlir:7-95).
 //
-// One workgroup (256 threads = 4 waves in a 2x2 grid) owns a 128x128 output
-// tile.  Main loop: the A and B k-tiles (128 bytes of K each) are fetched
-// with buffer loads whose out-of-range lanes read zero (no branches, so the
-// outstanding-load count stays exact), `PF` k-tiles ahead of use; B arrives
-// N-contiguous and is transposed in registers; both go to a two-stage LDS ring, and every wave
-// runs a 64x64 block of 32x32 MFMAs with f32 accumulation.  The MFMA is issued
-// as D = B^T . A^T so that each lane's accumulators belong to ONE output row:
-// row max / sum are then in-register, one cross-half swap, and one LDS
-// exchange between the two waves sharing the row.
+// One workgroup owns a TM x 128 output tile (TM = 128; 256 on the split
+// path of large problems).  16-bit and fp8 inputs: 512 threads = 8 waves of
+// 64 rows each (64x32 blocks in a 2x4 grid for TM = 128, 64x64 in a 4x2 grid
+// for TM = 256), 2 waves per SIMD; k-tiles of 128 bytes of K stream through
+// an LDS ring filled by direct-to-LDS buffer loads, B stays K-major in LDS
+// and its MFMA operands are read with LDS transpose reads.  f32 inputs:
+// 256 threads = 4 waves in a 2x2 grid; k-tiles are loaded `PF` ahead into
+// registers (out-of-range lanes read zero, so the outstanding-load count
+// stays exact), B is transposed in registers, and a two-stage LDS ring feeds
+// the MFMAs.  Accumulation is f32.  The MFMA is issued as D = B^T . A^T so
+// that each lane's accumulators belong to ONE output row: row max / sum are
+// then in-register, one cross-half swap, and one LDS exchange between the
+// waves sharing the row.
 //
 // Epilogues (template parameter EPI):
 //   kEpiExchange  single pass.  Every tile publishes its per-row (max, sumexp)
