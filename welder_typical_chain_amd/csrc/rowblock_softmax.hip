@@ -174,78 +174,94 @@ chain_rows_kernel(const ChainParams p) {
       areg[1][s] = read_a(1, s);
     }
 
-    // Pass-1 statistics of one tile (FULL: no column of the tile is past N).
-    auto ep1 = [&](auto full_c, const f32x16 (&acc)[2], int j) {
+    // Pass-1 statistics of one tile (FULL: no column of the tile is past N),
+    // in slices that a step spreads over its load groups: slice 0 the tile
+    // maxima of both m-subtiles, slice 1 + mt the exponential sum of m-subtile mt.
+    float nbase[2] = {0.0f, 0.0f}, nmax[2] = {0.0f, 0.0f};
+    auto ep1 = [&](auto full_c, auto slice_c, const f32x16 (&acc)[2], int j) {
       constexpr bool FULL = decltype(full_c)::value;
+      constexpr int SL = decltype(slice_c)::value;
       const int nvalid = (int)N - j * BN;
+      if constexpr (SL == 0) {
+        float mx[2];
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        float mx = NEG ? INFINITY : -INFINITY;
+        for (int mt = 0; mt < 2; ++mt) {
+          mx[mt] = NEG ? INFINITY : -INFINITY;
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const float x = FULL || nw + acc_i(lane, v) < nvalid ? acc[mt][v] : mx;
-          mx = NEG ? fminf(mx, x) : fmaxf(mx, x);
+          for (int v = 0; v < 16; ++v) {
+            const float x = FULL || nw + acc_i(lane, v) < nvalid ? acc[mt][v] : mx[mt];
+            mx[mt] = NEG ? fminf(mx[mt], x) : fmaxf(mx[mt], x);
+          }
         }
-        mx = NEG ? fminf(mx, __shfl_xor(mx, 32)) : fmaxf(mx, __shfl_xor(mx, 32));
-        const float tm = FULL ? mx * c2 : (mx == (NEG ? INFINITY : -INFINITY) ? -INFINITY : mx * c2);
-        const float nm = fmaxf(rm[mt], tm);
-        const float base = FULL ? nm : (nm == -INFINITY ? 0.0f : nm);  // all masked so far
-        float sm = rs[mt] * __builtin_amdgcn_exp2f(rm[mt] - base);
+        const float o0 = __shfl_xor(mx[0], 32), o1 = __shfl_xor(mx[1], 32);
+        mx[0] = NEG ? fminf(mx[0], o0) : fmaxf(mx[0], o0);
+        mx[1] = NEG ? fminf(mx[1], o1) : fmaxf(mx[1], o1);
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+          const float tm = FULL ? mx[mt] * c2 : (mx[mt] == (NEG ? INFINITY : -INFINITY) ? -INFINITY : mx[mt] * c2);
+          nmax[mt] = fmaxf(rm[mt], tm);
+          nbase[mt] = FULL ? nmax[mt] : (nmax[mt] == -INFINITY ? 0.0f : nmax[mt]);  // all masked so far
+        }
+      } else {
+        constexpr int mt = SL - 1;
+        const float base = nbase[mt];
+        float ps[4] = {rs[mt] * __builtin_amdgcn_exp2f(rm[mt] - base), 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[mt][v], c2, -base));
-          sm += FULL || nw + acc_i(lane, v) < nvalid ? e : 0.0f;
+          ps[v & 3] += FULL || nw + acc_i(lane, v) < nvalid ? e : 0.0f;
         }
-        rm[mt] = nm;
-        rs[mt] = sm;
+        rm[mt] = nmax[mt];
+        rs[mt] = (ps[0] + ps[1]) + (ps[2] + ps[3]);
       }
     };
-    // Pass-2 outputs of one tile: exp2(y - max - log2 sum), stored once.
-    auto ep2 = [&](const f32x16 (&acc)[2], int j) {
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        const uint32_t row = row0 + wm * 64 + mt * 32 + jr;
-        float o[16];
+    // Pass-2 outputs of one tile: exp2(y - max - log2 sum), stored once, in
+    // slices: 2*mt the exponentials of m-subtile mt (packed for 16-bit
+    // outputs), 2*mt + 1 their stores.
+    uint32_t pw[8];
+    float po[16];
+    auto ep2 = [&](auto slice_c, const f32x16 (&acc)[2], int j) {
+      constexpr int SL = decltype(slice_c)::value;
+      constexpr int mt = SL / 2;
+      const uint32_t row = row0 + wm * 64 + mt * 32 + jr;
+      if constexpr (SL % 2 == 0) {
 #pragma unroll
         for (int v = 0; v < 16; ++v)
-          o[v] = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[mt][v], c2, -gsub[mt]));
-        // lane l < 32 holds columns 8g + 0..3, lane l + 32 columns 8g + 4..7
-        // (g = 0..3) of the same row
-        if constexpr (OSZ == 4) {
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const uint32_t col = j * BN + nw + 8 * g + 4 * (lane >> 5);
-            const bool ok = row < M && col < N;
-            __builtin_amdgcn_raw_buffer_store_b128(
-                __builtin_bit_cast(u32x4, f32x4{o[4 * g], o[4 * g + 1], o[4 * g + 2], o[4 * g + 3]}),
-                ro, ok ? (int)(row * ldo + col * 4) : (int)kOutOfRange, 0, 0);
-          }
-        } else {
-          // pack to 16-bit pairs, then trade halves with lane ^ 32 so each
-          // lane holds two 16-byte runs: l < 32 columns 0-7 and 16-23,
-          // l >= 32 columns 8-15 and 24-31
-          uint32_t w[8];
+          po[v] = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[mt][v], c2, -gsub[mt]));
+        if constexpr (OSZ != 4) {
 #pragma unroll
           for (int g = 0; g < 4; ++g)
-            pack4<OUT_DT>(f32x4{o[4 * g], o[4 * g + 1], o[4 * g + 2], o[4 * g + 3]}, &w[2 * g],
-                          &w[2 * g + 1]);
-          const bool lo = lane < 32;
-          // send the groups the partner keeps: l < 32 sends g = 1, 3; l >= 32 sends g = 0, 2
-          const uint32_t s0 = lo ? w[2] : w[0], s1 = lo ? w[3] : w[1];
-          const uint32_t s2 = lo ? w[6] : w[4], s3 = lo ? w[7] : w[5];
-          const uint32_t r0 = __shfl_xor(s0, 32), r1 = __shfl_xor(s1, 32);
-          const uint32_t r2 = __shfl_xor(s2, 32), r3 = __shfl_xor(s3, 32);
-          const u32x4 run0 = lo ? u32x4{w[0], w[1], r0, r1} : u32x4{r0, r1, w[2], w[3]};
-          const u32x4 run1 = lo ? u32x4{w[4], w[5], r2, r3} : u32x4{r2, r3, w[6], w[7]};
-          const uint32_t c0 = j * BN + nw + (lo ? 0u : 8u);
+            pack4<OUT_DT>(f32x4{po[4 * g], po[4 * g + 1], po[4 * g + 2], po[4 * g + 3]}, &pw[2 * g],
+                          &pw[2 * g + 1]);
+        }
+      } else if constexpr (OSZ == 4) {
+        // lane l < 32 holds columns 8g + 0..3, lane l + 32 columns 8g + 4..7
 #pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            const uint32_t col = c0 + 16u * h;
-            const bool ok = row < M && col < N;
-            __builtin_amdgcn_raw_buffer_store_b128(h ? run1 : run0, ro,
-                                                   ok ? (int)(row * ldo + col * 2) : (int)kOutOfRange,
-                                                   0, 0);
-          }
+        for (int g = 0; g < 4; ++g) {
+          const uint32_t col = j * BN + nw + 8 * g + 4 * (lane >> 5);
+          const bool ok = row < M && col < N;
+          __builtin_amdgcn_raw_buffer_store_b128(
+              __builtin_bit_cast(u32x4, f32x4{po[4 * g], po[4 * g + 1], po[4 * g + 2], po[4 * g + 3]}),
+              ro, ok ? (int)(row * ldo + col * 4) : (int)kOutOfRange, 0, 0);
+        }
+      } else {
+        // trade halves with lane ^ 32 so each lane holds two 16-byte runs:
+        // l < 32 columns 0-7 and 16-23, l >= 32 columns 8-15 and 24-31
+        const bool lo = lane < 32;
+        const uint32_t s0 = lo ? pw[2] : pw[0], s1 = lo ? pw[3] : pw[1];
+        const uint32_t s2 = lo ? pw[6] : pw[4], s3 = lo ? pw[7] : pw[5];
+        const uint32_t r0 = __shfl_xor(s0, 32), r1 = __shfl_xor(s1, 32);
+        const uint32_t r2 = __shfl_xor(s2, 32), r3 = __shfl_xor(s3, 32);
+        const u32x4 run0 = lo ? u32x4{pw[0], pw[1], r0, r1} : u32x4{r0, r1, pw[2], pw[3]};
+        const u32x4 run1 = lo ? u32x4{pw[4], pw[5], r2, r3} : u32x4{r2, r3, pw[6], pw[7]};
+        const uint32_t c0 = j * BN + nw + (lo ? 0u : 8u);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const uint32_t col = c0 + 16u * h;
+          const bool ok = row < M && col < N;
+          __builtin_amdgcn_raw_buffer_store_b128(h ? run1 : run0, ro,
+                                                 ok ? (int)(row * ldo + col * 2) : (int)kOutOfRange,
+                                                 0, 0);
         }
       }
     };
@@ -266,32 +282,46 @@ chain_rows_kernel(const ChainParams p) {
       else
         wait_loads_barrier<BPW * (S - 2)>();
       __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int q = 0; q < BPW; ++q) issue_load(it + S - 1, q);
       const uint8_t* st = smem + RING_OFF + (it % S) * STAGE;
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) ACC[P][mt][v] = 0.0f;
-#pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        const u32x4 b = read_b(st, s);
-        ACC[P][0] = mfma16<IN_DT>(b, areg[0][s], ACC[P][0]);
-        ACC[P][1] = mfma16<IN_DT>(b, areg[1][s], ACC[P][1]);
-      }
       const int jp = (it - 1) % nT;
-      if constexpr (EP == 1) ep1(std::true_type{}, ACC[P ^ 1], jp);
-      if constexpr (EP == 2) ep1(std::false_type{}, ACC[P ^ 1], jp);
-      if constexpr (EP == 3) ep2(ACC[P ^ 1], jp);
-      if constexpr (EP != 0) {
+      using I0 = std::integral_constant<int, 0>;
+      using I1 = std::integral_constant<int, 1>;
+      using I2 = std::integral_constant<int, 2>;
+      using I3 = std::integral_constant<int, 3>;
+      // Group g: load g of tile it+S-1, the MFMAs of k-steps 2g, 2g+1 of tile
+      // it, and slice g of the epilogue of tile it-1.  A wave that issues a
+      // direct-to-LDS load waits until the memory pipeline takes it; with the
+      // loads spread over the step, the matrix core works through those waits.
+      auto group = [&](auto g_c) {
+        constexpr int g = decltype(g_c)::value;
+        static_assert(BPW == 4, "one load per group");
+        issue_load(it + S - 1, g);
 #pragma unroll
-        for (int i = 0; i < 2 * KS; ++i) {
-          __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // 2 LDS reads
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
-          __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // 6 VALU
+        for (int s2 = 0; s2 < 2; ++s2) {
+          const int s = 2 * g + s2;
+          const u32x4 b = read_b(st, s);
+          if (s == 0) {
+            f32x16 z;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) z[v] = 0.0f;
+            ACC[P][0] = mfma16<IN_DT>(b, areg[0][s], z);
+            ACC[P][1] = mfma16<IN_DT>(b, areg[1][s], z);
+          } else {
+            ACC[P][0] = mfma16<IN_DT>(b, areg[0][s], ACC[P][0]);
+            ACC[P][1] = mfma16<IN_DT>(b, areg[1][s], ACC[P][1]);
+          }
         }
-      }
-      __builtin_amdgcn_sched_barrier(0);
+        if constexpr (EP == 1 || EP == 2) {
+          using F = std::integral_constant<bool, EP == 1>;
+          if constexpr (g < 3) ep1(F{}, std::integral_constant<int, g>{}, ACC[P ^ 1], jp);
+        }
+        if constexpr (EP == 3) ep2(std::integral_constant<int, g>{}, ACC[P ^ 1], jp);
+        __builtin_amdgcn_sched_barrier(0);
+      };
+      group(I0{});
+      group(I1{});
+      group(I2{});
+      group(I3{});
     };
     using P0 = std::integral_constant<int, 0>;
     using P1 = std::integral_constant<int, 1>;
