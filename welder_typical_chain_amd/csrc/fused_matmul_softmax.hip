@@ -932,20 +932,27 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
 }
 
 // -------------------------------------------------------------------------
-// Second pass of the split (online two-pass) softmax: one wave per row.
-// Merges the row's nT tile statistics into (max, sum), then rescales the
-// tile-relative exponentials in place: out *= exp2(m_t - M) / S.
+// Second pass of the split (online two-pass) softmax.  `wpr` waves share a
+// row (the launcher picks it so that few, wide rows still give every CU
+// enough waves); wave `part` of a row takes its 16-byte chunks part, part +
+// wpr, ... in steps of 64 lanes.  Every wave merges the row's nT tile
+// statistics into (max, sum) itself, then rescales its chunks of the
+// tile-relative exponentials in place: out *= exp2(m_t - M) / S.  Four
+// chunks per lane are loaded before any is stored, so each lane keeps four
+// loads in flight.
 // -------------------------------------------------------------------------
 template <int OUT_DT>
 __global__ void __launch_bounds__(256)
 rescale_rows_kernel(uint8_t* __restrict__ out, const float2* __restrict__ partial,
                     int64_t rows_total, int64_t M, int64_t rows_pad, int64_t N,
-                    int64_t ldo_bytes, int64_t o_bstride, int nT) {
-  constexpr int ROWS_PER_WG = 4;
+                    int64_t ldo_bytes, int64_t o_bstride, int nT, int wpr) {
   constexpr int MAX_NT = 512;
-  __shared__ float fac[ROWS_PER_WG][MAX_NT];
+  constexpr int U = 4;  // chunks in flight per lane
+  __shared__ float fac[4][MAX_NT];
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int64_t grow = (int64_t)blockIdx.x * ROWS_PER_WG + w;  // row over batch*M
+  const int64_t gw = (int64_t)blockIdx.x * 4 + w;  // global wave
+  const int64_t grow = gw / wpr;                   // row over batch*M
+  const int part = (int)(gw - grow * wpr);
   const bool live = grow < rows_total;
   int64_t bt = 0, m = 0;
   if (live) {
@@ -969,10 +976,9 @@ rescale_rows_kernel(uint8_t* __restrict__ out, const float2* __restrict__ partia
   constexpr int OSZ = OutTraits<OUT_DT>::SZ;
   constexpr int EPC = 16 / OSZ;
   uint8_t* rowp = out + bt * o_bstride + m * ldo_bytes;
-  for (int64_t c = lane; c * EPC < N; c += 64) {
-    const int64_t n = c * EPC;
-    const float f = fac[w][n / BN];
-    u32x4 u = *reinterpret_cast<const u32x4*>(rowp + n * OSZ);
+  const int64_t nch = N / EPC;                 // 16-byte chunks in the row
+  const int64_t step = (int64_t)64 * wpr;      // chunks between a lane's consecutive chunks
+  auto scale = [&](u32x4 u, float f) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const uint32_t x = u[e];
@@ -994,7 +1000,22 @@ rescale_rows_kernel(uint8_t* __restrict__ out, const float2* __restrict__ partia
       }
       u[e] = y;
     }
-    *reinterpret_cast<u32x4*>(rowp + n * OSZ) = u;
+    return u;
+  };
+  int64_t c = (int64_t)part * 64 + lane;
+  for (; c + (U - 1) * step < nch; c += U * step) {
+    u32x4 v[U];
+#pragma unroll
+    for (int i = 0; i < U; ++i) v[i] = *reinterpret_cast<const u32x4*>(rowp + (c + i * step) * 16);
+#pragma unroll
+    for (int i = 0; i < U; ++i) {
+      const int64_t n = (c + i * step) * EPC;
+      *reinterpret_cast<u32x4*>(rowp + (c + i * step) * 16) = scale(v[i], fac[w][n / BN]);
+    }
+  }
+  for (; c < nch; c += step) {
+    const int64_t n = c * EPC;
+    *reinterpret_cast<u32x4*>(rowp + c * 16) = scale(*reinterpret_cast<const u32x4*>(rowp + c * 16), fac[w][n / BN]);
   }
 }
 

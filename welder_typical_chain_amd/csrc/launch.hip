@@ -391,9 +391,12 @@ int wtc_matmul_softmax(const void* a, const void* b, void* out, int64_t batch, i
     int64_t rows_total = batch * m, M_ = m, rows_pad = (int64_t)p.nRB * tile_rows, N_ = n,
             ldo = p.ldo_bytes, ob = p.o_bstride;
     int nT = p.nT;
-    void* args[] = {&o, &part, &rows_total, &M_, &rows_pad, &N_, &ldo, &ob, &nT};
+    // waves per row: enough waves for 16 per CU when rows are few, at most 8
+    int wpr = 1;
+    while (wpr < 8 && rows_total * wpr < 16ll * ds->cu_count) wpr *= 2;
+    void* args[] = {&o, &part, &rows_total, &M_, &rows_pad, &N_, &ldo, &ob, &nT, &wpr};
     HIP_TRY(hipLaunchKernel(rescale_kernel_symbol(out_dtype),
-                            dim3((unsigned)ceil_div(rows_total, kRescaleRowsPerWg)), dim3(256),
+                            dim3((unsigned)ceil_div(rows_total * wpr, kRescaleRowsPerWg)), dim3(256),
                             args, 0, stream));
     return WTC_OK;
   }
