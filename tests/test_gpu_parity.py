@@ -213,3 +213,47 @@ def test_exchange_repeated_launches_and_workspace_reuse(native_lib):
     flags, longest, timeouts = read_diagnostics(ws)
     print(f"[gpu-case] worst rel err {worst:.3e}; longest wait {longest / 100:.1f} us; timeouts {timeouts}")
     assert worst < 2e-3 and flags == 0 and timeouts == 0
+
+
+@needs_gpu
+@pytest.mark.parametrize("path,shape,in_dt", [("exchange", (1, 1024, 2048, 256), torch.float16),
+                                              ("split", (1, 512, 4096, 256), torch.bfloat16),
+                                              ("rows", (4, 512, 1024, 128), torch.float16),
+                                              ("unfused", (1, 256, 512, 128), torch.float16)])
+def test_graph_replay_matches_eager(native_lib, path, shape, in_dt):
+    """Calls captured in a HIP graph (torch.cuda.graph) and replayed several
+    times, with the program's own eager work and synchronisations between the
+    replays, give the eager call's output bit for bit on every replay: the
+    launches keep no per-launch host state and record no memset."""
+    from welder_typical_chain_amd.chain import matmul_softmax, new_workspace, workspace_size
+    batch, m, n, k = shape
+    _announce(f"graph replay path={path} batch={batch} {m}x{n}x{k} {in_dt}")
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev)
+    g.manual_seed(11)
+    bs = (batch,) if batch > 1 else ()
+    a = (torch.randn((*bs, m, k), generator=g, device=dev) / k ** 0.5).to(in_dt)
+    b = (torch.randn((*bs, k, n), generator=g, device=dev)).to(in_dt)
+    code = {torch.float16: 1, torch.bfloat16: 2}[in_dt]
+    ws = new_workspace(workspace_size(batch, m, n, k, code, 1, path), dev)
+    out = torch.empty((*bs, m, n), dtype=torch.float16, device=dev)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(3):  # eager warm-up (library initialisation happens outside capture)
+            matmul_softmax(a, b, out=out, path=path, workspace=ws)
+    torch.cuda.synchronize()
+    ref = out.clone()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        matmul_softmax(a, b, out=out, path=path, workspace=ws)
+        matmul_softmax(a, b, out=out, path=path, workspace=ws)
+    torch.cuda.synchronize()
+    for rep in range(4):
+        out.zero_()
+        junk = (a.float() * 2.0).sum()  # eager work between replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), f"replay {rep}: max diff {(out.float() - ref.float()).abs().max().item()}"
+        del junk
