@@ -6,6 +6,9 @@
   ``libwelder-solver-capi.so`` (CPU only: chain recogniser + tile solver): the
   file names the reference's toolchain looks for in its backend build
   directory (reference compiler/backend/Toolchain.cpp:29-45).
+- ``wtc-compiler``: the reference's pipeline driver CLI (``--search-only``,
+  ``--compile-only``, full) over the two C-ABIs, linked against
+  ``libwtc_hip.so`` next to it.
 - ``<source>.gfx950.co``: the device code object of each HIP source, and
   ``kernel_resources.json``: per kernel, the register / LDS / scratch figures
   from the code object's metadata and instruction counts (MFMA, LDS DMA,
@@ -29,6 +32,7 @@ OBJ = PKG / "_build"
 LIB = PKG / "libwtc_hip.so"
 COMPILE_LIB = PKG / "libwelder-compile-capi.so"
 SOLVER_LIB = PKG / "libwelder-solver-capi.so"
+CLI = PKG / "wtc-compiler"
 RESOURCES = PKG / "kernel_resources.json"
 RESOURCES_TSV = PKG / "kernel_resources.tsv"
 TSV_COLUMNS = ["vgpr_count", "agpr_count", "sgpr_count", "vgpr_spill_count", "sgpr_spill_count",
@@ -158,6 +162,11 @@ def build(verbose: bool = False) -> Path:
     tmp = SOLVER_LIB.with_suffix(".so.tmp")
     _run(["g++", "-shared", "-Wl,--no-undefined", "-o", str(tmp), *cpu_objs])
     os.replace(tmp, SOLVER_LIB)
+    rocm_lib = str(Path(os.environ.get("ROCM_PATH", "/opt/rocm")) / "lib")
+    tmp = CLI.with_suffix(".tmp")
+    _run(["g++", *CXX_FLAGS, str(CSRC / "wtc_compiler.cpp"), "-o", str(tmp), f"-L{PKG}", "-lwtc_hip",
+          f"-Wl,-rpath-link,{rocm_lib}", "-Wl,-rpath,$ORIGIN"])
+    os.replace(tmp, CLI)
     res = _kernel_resources(code_objects)
     RESOURCES.write_text(json.dumps(res, indent=1, sort_keys=True) + "\n")
     # the same figures as a flat table for the compile C-ABI's report

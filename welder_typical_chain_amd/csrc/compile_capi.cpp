@@ -24,6 +24,7 @@ namespace wtc {
 int chain_kernel_threads(int in_dt);
 int rows_kernel_threads();
 int split_tile_rows(int in_dt, int64_t batch, int64_t m, int64_t n, int cu_count);
+int rescale_waves_per_row(int64_t rows_total, int cu_count);
 
 static std::string library_path() {
   Dl_info info{};
@@ -168,7 +169,7 @@ static int compile_impl(const char* input_mlir_path, const char* out_dir, int64_
     ks.push_back({"chain_tile_kernel<" + kin + "," + kout + ",split," + std::to_string(tm) + "x128>",
                   chain_sym(in_code, out_code, 1, tm), grid, 0, tile_threads});
     ks.push_back({"rescale_rows_kernel<" + kout + ">", "_ZN3wtc19rescale_rows_kernel" + out_t,
-                  (rows + 3) / 4, 8192});
+                  (rows * rescale_waves_per_row(rows, 256) + 3) / 4, 8192});
   } else {
     ks.push_back({"chain_tile_kernel<" + kin + ",f32,logits>", chain_sym(in_code, 0, 2), grid, 0,
                   tile_threads});

@@ -18,6 +18,14 @@
 // no padding rows (an even number of 128-row blocks) and the problem still
 // gives every CU at least two of them; 128 otherwise.
 namespace wtc {
+// Waves of rescale_rows_kernel per row: enough for 16 waves per CU when rows
+// are few (wide rows), at most 8.
+int rescale_waves_per_row(int64_t rows_total, int cu_count) {
+  int wpr = 1;
+  while (wpr < 8 && rows_total * wpr < 16ll * cu_count) wpr *= 2;
+  return wpr;
+}
+
 int split_tile_rows(int in_dt, int64_t batch, int64_t m, int64_t n, int cu_count) {
   if (in_dt == DT_F32) return 128;
   const int64_t rb128 = (m + 127) / 128;
@@ -391,9 +399,7 @@ int wtc_matmul_softmax(const void* a, const void* b, void* out, int64_t batch, i
     int64_t rows_total = batch * m, M_ = m, rows_pad = (int64_t)p.nRB * tile_rows, N_ = n,
             ldo = p.ldo_bytes, ob = p.o_bstride;
     int nT = p.nT;
-    // waves per row: enough waves for 16 per CU when rows are few, at most 8
-    int wpr = 1;
-    while (wpr < 8 && rows_total * wpr < 16ll * ds->cu_count) wpr *= 2;
+    int wpr = rescale_waves_per_row(rows_total, ds->cu_count);
     void* args[] = {&o, &part, &rows_total, &M_, &rows_pad, &N_, &ldo, &ob, &nT, &wpr};
     HIP_TRY(hipLaunchKernel(rescale_kernel_symbol(out_dtype),
                             dim3((unsigned)ceil_div(rows_total * wpr, kRescaleRowsPerWg)), dim3(256),

@@ -1,0 +1,440 @@
+// wtc_compiler.cpp -- the wtc-compiler command line: the typical-chain
+// pipeline driver of the reference (options of compiler/main.cpp:10-90,
+// stages of compiler/pipeline/PipelineRunner.cpp:52-219) over this library.
+//
+// Stages and output layout (<out>/ir, <out>/search, <out>/{fused|baseline})
+// follow the reference; what runs in each stage is this build's own:
+//   canonicalize  text-level recognition of the chain (no mlir-opt) and the
+//                 canonical decomposed form  -> ir/01.canonicalized.mlir, .log
+//   tagging       wtc.tag comments + tags JSON -> ir/02.tagged.mlir, 02.tags.json
+//   search        welder_solver_solve_typical_chain over the gfx950 kernel
+//                 variants -> search/best_summary.json, candidates.tsv, solver.log
+//                 (skipped with --best-json or --no-search), then tile overrides
+//                 and search/best.json
+//   compile       welder_compile_typical_chain_to_nvvm -> <dir>/03..05, kernel_report.txt
+//   validate      the artefacts exist and are non-empty -> postbufferize_report.txt
+// Modes: full (all stages), --search-only (stop after best.json),
+// --compile-only (the reference's semantics: search only when no tiles are given).
+// --backend-root / --backend-mode / --pure-api-full are accepted for
+// compatibility; there is one in-process backend.
+#include <cstdint>
+#include <cstdlib>
+#include <filesystem>
+#include <iostream>
+#include <sstream>
+#include <string>
+
+#include "chain_spec.h"
+#include "wtc/welder_compile_capi.h"
+#include "wtc/welder_solver_capi.h"
+
+namespace {
+
+namespace fs = std::filesystem;
+
+enum class Mode { Full, SearchOnly, CompileOnly };
+
+struct Options {
+  std::string input;
+  std::string output_dir = "/tmp/wtc_out";
+  std::string backend_root;
+  std::string backend_mode = "process_chain";
+  std::string best_json;
+  int64_t max_connect_level = 1;
+  wtc::TileParams override_tiles;
+  bool enable_search = true;
+  bool fused = true;
+  bool pure_api_full = false;
+  Mode mode = Mode::Full;
+  bool verbose = false;
+};
+
+int count_of(const std::string& text, const char* needle) {
+  int n = 0;
+  const std::string nd(needle);
+  for (size_t p = text.find(nd); p != std::string::npos; p = text.find(nd, p + nd.size())) ++n;
+  return n;
+}
+
+bool contains(const std::string& text, const char* needle) {
+  return text.find(needle) != std::string::npos;
+}
+
+// Stage 1.  The reference runs mlir-opt --canonicalize (after decomposing a
+// named linalg.softmax) and checks that matmul, exp and divf survive
+// (compiler/ir/ChainCanonicalize.cpp:77-163); here the chain is recognised
+// from the text and re-emitted in canonical decomposed form, then the same
+// checks run on the result.
+bool canonicalize(const std::string& input, const fs::path& out_mlir, wtc::ChainSpec& spec,
+                  std::string& diag) {
+  std::string text;
+  if (!fs::exists(input)) {
+    diag = "input file not found: " + input;
+    return false;
+  }
+  if (!wtc::read_file(input, text) || text.empty()) {
+    diag = "failed to read input MLIR: " + input;
+    return false;
+  }
+  std::string why;
+  const bool ok = wtc::recognize_chain(text, spec, why);
+  std::ostringstream log;
+  log << "[wtc canonicalize] input " << input << "\n";
+  if (!ok) {
+    log << "[wtc canonicalize] not a Matmul -> row-Softmax chain: " << why << "\n";
+    wtc::write_file((out_mlir.parent_path() / "01.canonicalize.log").string(), log.str());
+    diag = "chain not recognised: " + why + ", see " +
+           (out_mlir.parent_path() / "01.canonicalize.log").string();
+    return false;
+  }
+  const std::string canonical = wtc::emit_canonical_mlir(spec);
+  log << "[wtc canonicalize] batch=" << spec.batch << " m=" << spec.m << " n=" << spec.n
+      << " k=" << spec.k << " in=" << wtc::elem_mlir_name(spec.in)
+      << " acc=" << wtc::elem_mlir_name(spec.acc) << " out=" << wtc::elem_mlir_name(spec.out)
+      << " softmax=" << (spec.form == wtc::SoftmaxForm::Named ? "named (decomposed)" : "decomposed")
+      << " logit_scale=" << spec.logit_scale
+      << (spec.runtime_scales ? " runtime_scales" : "") << "\n";
+  if (!wtc::write_file(out_mlir.string(), canonical) ||
+      !wtc::write_file((out_mlir.parent_path() / "01.canonicalize.log").string(), log.str())) {
+    diag = "failed to write " + out_mlir.string();
+    return false;
+  }
+  if (!contains(canonical, "linalg.matmul") && !contains(canonical, "linalg.batch_matmul")) {
+    diag = "canonicalized IR lost linalg.matmul unexpectedly";
+    return false;
+  }
+  if (contains(canonical, "linalg.softmax")) {
+    diag = "softmax decomposition did not run: linalg.softmax remains";
+    return false;
+  }
+  if (!contains(canonical, "math.exp") || !contains(canonical, "arith.divf")) {
+    diag = "canonicalized IR does not contain expected softmax decomposition ops";
+    return false;
+  }
+  return true;
+}
+
+// Stage 2 (compiler/ir/Tagging.cpp:50-159): tags the canonicalized file.
+bool tag(const fs::path& canonical_path, const wtc::ChainSpec& spec, const fs::path& tagged_path,
+         const fs::path& tags_json_path, std::string& diag) {
+  std::string text;
+  if (!wtc::read_file(canonical_path.string(), text) || text.empty()) {
+    diag = "failed to read input MLIR for tagging: " + canonical_path.string();
+    return false;
+  }
+  if ((count_of(text, "linalg.matmul") + count_of(text, "linalg.batch_matmul")) == 0 ||
+      count_of(text, "linalg.generic") == 0) {
+    diag = "tagging expects matmul + generic softmax decomposition in input";
+    return false;
+  }
+  std::string tagged, tags_json;
+  wtc::tag_chain(text, spec, canonical_path.string(), tagged, tags_json);
+  if (!wtc::write_file(tagged_path.string(), tagged)) {
+    diag = "failed to write tagged MLIR: " + tagged_path.string();
+    return false;
+  }
+  if (!wtc::write_file(tags_json_path.string(), tags_json)) {
+    diag = "failed to write tags json: " + tags_json_path.string();
+    return false;
+  }
+  return true;
+}
+
+// The validation stage (compiler/runtime/PostbufferizeFixups.cpp:33-89),
+// re-targeted to the HIP artefacts: counts from the canonical IR, the launch
+// plan and the kernel report instead of post-bufferize IR, gpu.launch and PTX.
+bool validate(const fs::path& dir, std::string& diag) {
+  const fs::path canonical = dir / "03.chain.canonical.mlir";
+  const fs::path plan = dir / "04.kernel.plan.json";
+  const fs::path launch = dir / "05.out.hip.launch.json";
+  const fs::path kreport = dir / "kernel_report.txt";
+  if (!fs::exists(canonical) || !fs::exists(plan) || !fs::exists(launch)) {
+    diag = "expected compiler artifacts are missing under " + dir.string();
+    return false;
+  }
+  std::string c, p, l, k;
+  if (!wtc::read_file(canonical.string(), c) || !wtc::read_file(plan.string(), p) ||
+      !wtc::read_file(launch.string(), l) || c.empty() || p.empty() || l.empty()) {
+    diag = "failed to read compiler artifacts under " + dir.string();
+    return false;
+  }
+  wtc::read_file(kreport.string(), k);
+  auto report_value = [&](const char* key) -> std::string {
+    const std::string needle = std::string(key) + "=";
+    const size_t at = k.find(needle);
+    if (at == std::string::npos) return "0";
+    const size_t end = k.find('\n', at);
+    return k.substr(at + needle.size(), end == std::string::npos ? std::string::npos
+                                                                 : end - at - needle.size());
+  };
+  std::ostringstream r;
+  r << "post_matmul_count=" << count_of(c, "linalg.matmul") + count_of(c, "linalg.batch_matmul")
+    << "\n";
+  r << "launch_kernel_count=" << count_of(p, "\"name\":") << "\n";
+  r << "launch_scratch_bytes=" << report_value("scratch_bytes") << "\n";
+  r << "mfma_instruction_count=" << report_value("mfma_instruction_count") << "\n";
+  r << "scratch_instruction_count=" << report_value("scratch_instruction_count") << "\n";
+  r << "vgpr_spill_count=" << report_value("vgpr_spill_count") << "\n";
+  if (!wtc::write_file((dir / "postbufferize_report.txt").string(), r.str())) {
+    diag = "failed to write postbufferize report: " + (dir / "postbufferize_report.txt").string();
+    return false;
+  }
+  return true;
+}
+
+bool any_override(const wtc::TileParams& t) {
+  return t.tile_m > 0 || t.tile_n > 0 || t.tile_k > 0 || t.thread_tile_m > 0 ||
+         t.thread_tile_n > 0;
+}
+
+int run_pipeline(const Options& o) {
+  std::string diag;
+  if (o.output_dir.empty()) {
+    std::cerr << "error: output dir is empty\n";
+    return 1;
+  }
+  const fs::path root = o.output_dir;
+  const fs::path ir = root / "ir", search = root / "search";
+  const fs::path compile_dir = root / (o.fused ? "fused" : "baseline");
+  std::error_code ec;
+  fs::create_directories(ir, ec);
+  if (ec) {
+    std::cerr << "error: cannot create " << ir << "\n";
+    return 1;
+  }
+
+  if (o.verbose) std::cout << "[wtc] phase: canonicalize\n";
+  wtc::ChainSpec spec;
+  const fs::path canonical = ir / "01.canonicalized.mlir";
+  if (!canonicalize(o.input, canonical, spec, diag)) {
+    std::cerr << "error: canonicalize failed: " << diag << "\n";
+    return 1;
+  }
+  if (o.verbose) std::cout << "[wtc] phase: tagging\n";
+  const fs::path tagged = ir / "02.tagged.mlir";
+  if (!tag(canonical, spec, tagged, ir / "02.tags.json", diag)) {
+    std::cerr << "error: tagging failed: " << diag << "\n";
+    return 1;
+  }
+
+  fs::create_directories(search, ec);
+  // The backend consumes the canonicalized + tagged input, as in the reference.
+  const std::string backend_input = tagged.string();
+  wtc::TileParams best;
+  bool have_best = false;
+  if (!o.best_json.empty()) {
+    if (o.verbose) std::cout << "[wtc] load best json: " << o.best_json << "\n";
+    if (!wtc::load_best_json(o.best_json, best, diag)) {
+      std::cerr << "error: failed to load --best-json: " << diag << "\n";
+      return 1;
+    }
+    have_best = true;
+  }
+  if (!have_best && o.enable_search) {
+    if (o.verbose) std::cout << "[wtc] phase: search (in-process solver)\n";
+    const fs::path summary = search / "best_summary.json", candidates = search / "candidates.tsv";
+    const fs::path solver_log = search / "solver.log";
+    char err[4096];
+    const int rc = welder_solver_solve_typical_chain(
+        backend_input.c_str(), summary.c_str(), candidates.c_str(), o.max_connect_level,
+        o.verbose ? 1 : 0, &best.tile_m, &best.tile_n, &best.tile_k, &best.thread_tile_m,
+        &best.thread_tile_n, err, sizeof err);
+    std::ostringstream log;
+    log << "[wtc.search] input=" << backend_input << "\n[wtc.search] max_connect_level="
+        << o.max_connect_level << "\n[wtc.search] rc=" << rc << (rc ? std::string(" error=") + err : "")
+        << "\n";
+    wtc::write_file(solver_log.string(), log.str());
+    if (rc != 0) {
+      std::cerr << "error: search failed: backend solver failed, rc=" << rc << ", error=" << err
+                << ", see " << solver_log.string() << "\n";
+      return 1;
+    }
+    have_best = true;
+    if (o.verbose) {
+      std::cout << "[wtc] search best: " << (search / "best.json").string() << "\n";
+      std::cout << "[wtc] search candidates: " << candidates.string() << "\n";
+    }
+  }
+  if (any_override(o.override_tiles)) {
+    if (o.verbose) std::cout << "[wtc] apply tile overrides\n";
+    const wtc::TileParams& t = o.override_tiles;
+    if (t.tile_m > 0) best.tile_m = t.tile_m;
+    if (t.tile_n > 0) best.tile_n = t.tile_n;
+    if (t.tile_k > 0) best.tile_k = t.tile_k;
+    if (t.thread_tile_m > 0) best.thread_tile_m = t.thread_tile_m;
+    if (t.thread_tile_n > 0) best.thread_tile_n = t.thread_tile_n;
+    have_best = true;
+  }
+  if (!have_best && o.mode == Mode::SearchOnly) {
+    std::cerr << "error: search-only mode has no result. Provide --best-json or enable search.\n";
+    return 1;
+  }
+  if (!have_best) {
+    // search disabled and no tiles given: the library's default variant for the input type
+    best = wtc::supported_variants(spec.in).front().tiles;
+    if (o.verbose) std::cout << "[wtc] search disabled, using built-in default tiles\n";
+  }
+  const fs::path best_path = search / "best.json";
+  if (!wtc::write_best_json(best, best_path.string(), diag)) {
+    std::cerr << "error: failed to persist best.json: " << diag << "\n";
+    return 1;
+  }
+  if (o.verbose)
+    std::cout << "[wtc] selected tile=(" << best.tile_m << "x" << best.tile_n << "x" << best.tile_k
+              << ") thread_tile=(" << best.thread_tile_m << "x" << best.thread_tile_n << ")\n";
+  if (o.mode == Mode::SearchOnly) {
+    std::cout << "[wtc] search completed. best: " << best_path.string() << "\n";
+    return 0;
+  }
+
+  if (o.verbose) std::cout << "[wtc] phase: build + compile (gfx950)\n";
+  fs::create_directories(compile_dir, ec);
+  char err[4096];
+  const int rc = welder_compile_typical_chain_to_nvvm(
+      backend_input.c_str(), compile_dir.c_str(), "", "", best.tile_m, best.tile_n, best.tile_k,
+      best.thread_tile_m, best.thread_tile_n, o.fused ? o.max_connect_level : 0, o.fused ? 1 : 0,
+      o.verbose ? 1 : 0, err, sizeof err);
+  std::ostringstream clog;
+  clog << "[wtc.compile] input=" << backend_input << " out=" << compile_dir.string()
+       << " fused=" << (o.fused ? 1 : 0) << " tiles=" << best.tile_m << "x" << best.tile_n << "x"
+       << best.tile_k << "/" << best.thread_tile_m << "x" << best.thread_tile_n << " rc=" << rc
+       << (rc ? std::string(" error=") + err : "") << "\n";
+  wtc::write_file((compile_dir / "compile.log").string(), clog.str());
+  if (rc != 0) {
+    std::cerr << "error: build/compile failed: welder_compile_typical_chain_to_nvvm rc=" << rc
+              << ": " << err << "\n";
+    return 1;
+  }
+  if (o.verbose) std::cout << "[wtc] phase: validate artifacts\n";
+  if (!validate(compile_dir, diag)) {
+    std::cerr << "error: artifact validation failed: " << diag << "\n";
+    return 1;
+  }
+  std::cout << "[wtc] pipeline completed. artifact: "
+            << (compile_dir / "05.out.hip.launch.json").string() << "\n";
+  return 0;
+}
+
+void usage() {
+  std::cout << "Usage: wtc-compiler --input <mlir-file> [options]\n"
+            << "Options:\n"
+            << "  --output-dir <dir>       Output root dir (default /tmp/wtc_out)\n"
+            << "  --backend-root <dir>     Accepted for compatibility (one in-process backend)\n"
+            << "  --backend-mode <mode>    shell|process_chain|api, accepted for compatibility\n"
+            << "  --pure-api-full          Accepted for compatibility\n"
+            << "  --legacy-root <dir>      Alias of --backend-root\n"
+            << "  --search-only            Run solver only and dump search artifacts\n"
+            << "  --compile-only           Skip solver (unless no tiles provided) and compile\n"
+            << "  --best-json <path>       Read tile result from json (tileM/N/K/threadTileM/N)\n"
+            << "  --tile-m <n>             Override tileM\n"
+            << "  --tile-n <n>             Override tileN\n"
+            << "  --tile-k <n>             Override tileK\n"
+            << "  --thread-tile-m <n>      Override threadTileM\n"
+            << "  --thread-tile-n <n>      Override threadTileN\n"
+            << "  --max-connect-level <n>  Connect level for the fused path\n"
+            << "  --no-search              Do not run solver search\n"
+            << "  --repeat <n>             Repeat in one process (stress reentrancy)\n"
+            << "  --baseline               Compile baseline (unfused) variant\n"
+            << "  --fused                  Compile fused variant (default)\n"
+            << "  --verbose                Verbose logs\n";
+}
+
+bool parse_int(const char* s, int64_t& v) {
+  try {
+    size_t used = 0;
+    v = std::stoll(s, &used);
+    return used == std::string(s).size();
+  } catch (...) {
+    return false;
+  }
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+  Options o;
+  int64_t repeat = 1;
+  for (int i = 1; i < argc; ++i) {
+    const std::string arg = argv[i];
+    const bool has_value = i + 1 < argc;
+    auto int_arg = [&](int64_t& dst) {
+      if (!parse_int(argv[++i], dst)) {
+        std::cerr << "error: " << arg << " expects an integer, got '" << argv[i] << "'\n";
+        std::exit(2);
+      }
+    };
+    if (arg == "--input" && has_value) {
+      o.input = argv[++i];
+    } else if ((arg == "--output-dir" || arg == "--out-dir") && has_value) {
+      o.output_dir = argv[++i];
+    } else if ((arg == "--backend-root" || arg == "--legacy-root") && has_value) {
+      o.backend_root = argv[++i];
+    } else if (arg == "--best-json" && has_value) {
+      o.best_json = argv[++i];
+    } else if (arg == "--backend-mode" && has_value) {
+      const std::string m = argv[++i];
+      if (m != "shell" && m != "process_chain" && m != "api") {
+        std::cerr << "error: unknown backend mode '" << m << "' (shell|process_chain|api)\n";
+        return 2;
+      }
+      o.backend_mode = m;
+    } else if (arg == "--max-connect-level" && has_value) {
+      int_arg(o.max_connect_level);
+    } else if (arg == "--tile-m" && has_value) {
+      int_arg(o.override_tiles.tile_m);
+    } else if (arg == "--tile-n" && has_value) {
+      int_arg(o.override_tiles.tile_n);
+    } else if (arg == "--tile-k" && has_value) {
+      int_arg(o.override_tiles.tile_k);
+    } else if (arg == "--thread-tile-m" && has_value) {
+      int_arg(o.override_tiles.thread_tile_m);
+    } else if (arg == "--thread-tile-n" && has_value) {
+      int_arg(o.override_tiles.thread_tile_n);
+    } else if (arg == "--no-search") {
+      o.enable_search = false;
+    } else if (arg == "--pure-api-full") {
+      o.pure_api_full = true;
+    } else if (arg == "--repeat" && has_value) {
+      int_arg(repeat);
+    } else if (arg == "--search-only") {
+      o.mode = Mode::SearchOnly;
+    } else if (arg == "--compile-only") {
+      o.mode = Mode::CompileOnly;
+    } else if (arg == "--baseline") {
+      o.fused = false;
+      if (o.max_connect_level > 0) o.max_connect_level = 0;
+    } else if (arg == "--fused") {
+      o.fused = true;
+    } else if (arg == "--verbose") {
+      o.verbose = true;
+    } else if (arg == "--help" || arg == "-h") {
+      usage();
+      return 0;
+    } else {
+      std::cerr << "Unknown argument: " << arg << "\n";
+      return 2;
+    }
+  }
+  if (o.input.empty()) {
+    std::cerr << "error: --input is required\n";
+    return 2;
+  }
+  if (repeat <= 0) {
+    std::cerr << "error: --repeat must be >= 1\n";
+    return 2;
+  }
+  if (repeat == 1) return run_pipeline(o);
+  for (int64_t i = 0; i < repeat; ++i) {
+    Options it = o;
+    it.output_dir = (fs::path(o.output_dir) / ("iter_" + std::to_string(i))).string();
+    if (o.verbose)
+      std::cout << "[wtc] repeat " << (i + 1) << "/" << repeat << ", output-dir=" << it.output_dir
+                << "\n";
+    const int rc = run_pipeline(it);
+    if (rc != 0) {
+      std::cerr << "error: repeat iteration failed at i=" << i << ", rc=" << rc << "\n";
+      return rc;
+    }
+  }
+  return 0;
+}

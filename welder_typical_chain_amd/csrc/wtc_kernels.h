@@ -38,6 +38,8 @@ struct ChainParams {
 // tile_rows: 128, or 256 for the split path with 16-bit or fp8 inputs (else NULL).
 const void* chain_kernel_symbol(int in_dt, int out_dt, int epi, int tile_rows = 128);
 const void* rescale_kernel_symbol(int out_dt);
+// Waves that share one row in rescale_rows_kernel (its grid is rows * wpr / 4).
+int rescale_waves_per_row(int64_t rows_total, int cu_count);
 const void* zero_kernel_symbol();
 int chain_kernel_lds_bytes(int in_dt, int out_dt);
 // Tile height (128 or 256) the split path uses for this problem on a device
