@@ -272,9 +272,10 @@ chain_rows_kernel(const ChainParams p) {
     // all in one basic block so that the scheduler interleaves the
     // epilogue's VALU work with the MFMAs (the matrix core runs an MFMA for
     // 32 cycles while the wave issues other instructions).
-    auto step = [&](auto par_c, auto ep_c, int it) {
+    auto step = [&](auto par_c, auto ep_c, int it, auto mma_c) {
       constexpr int P = decltype(par_c)::value;
       constexpr int EP = decltype(ep_c)::value;
+      constexpr bool MMA = decltype(mma_c)::value;  // false: the stream's last step (no tile `it`)
       __builtin_amdgcn_sched_barrier(0);
       // tile it landed; every wave is done with stage (it-1)%S
       if (it >= nT + 2)
@@ -297,7 +298,7 @@ chain_rows_kernel(const ChainParams p) {
         static_assert(BPW == 4, "one load per group");
         issue_load(it + S - 1, g);
 #pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
+        for (int s2 = 0; s2 < (MMA ? 2 : 0); ++s2) {
           const int s = 2 * g + s2;
           const u32x4 b = read_b(st, s);
           if (s == 0) {
@@ -329,15 +330,16 @@ chain_rows_kernel(const ChainParams p) {
       return (int)N - ((it - 1) % nT) * BN >= BN;
     };
 
-    step(P0{}, std::integral_constant<int, 0>{}, 0);
+    using Y = std::true_type;
+    step(P0{}, std::integral_constant<int, 0>{}, 0, Y{});
     for (int it = 1; it <= nT; ++it) {
       const bool full = pass1_ep(it);
       if (it & 1) {
-        if (full) step(P1{}, std::integral_constant<int, 1>{}, it);
-        else step(P1{}, std::integral_constant<int, 2>{}, it);
+        if (full) step(P1{}, std::integral_constant<int, 1>{}, it, Y{});
+        else step(P1{}, std::integral_constant<int, 2>{}, it, Y{});
       } else {
-        if (full) step(P0{}, std::integral_constant<int, 1>{}, it);
-        else step(P0{}, std::integral_constant<int, 2>{}, it);
+        if (full) step(P0{}, std::integral_constant<int, 1>{}, it, Y{});
+        else step(P0{}, std::integral_constant<int, 2>{}, it, Y{});
       }
     }
     // Merge the 4 column-waves of each row.  The statistics go to the stage
@@ -370,10 +372,13 @@ chain_rows_kernel(const ChainParams p) {
       }
       gsub[mt] = gm + __builtin_amdgcn_logf(gs);  // v_log_f32 is log2
     }
-    for (int it = nT + 1; it <= total; ++it) {
-      if (it & 1) step(P1{}, std::integral_constant<int, 3>{}, it);
-      else step(P0{}, std::integral_constant<int, 3>{}, it);
+    for (int it = nT + 1; it < total; ++it) {
+      if (it & 1) step(P1{}, std::integral_constant<int, 3>{}, it, Y{});
+      else step(P0{}, std::integral_constant<int, 3>{}, it, Y{});
     }
+    // the last step only stores tile total-1 (there is no tile `total`)
+    if (total & 1) step(P1{}, std::integral_constant<int, 3>{}, total, std::false_type{});
+    else step(P0{}, std::integral_constant<int, 3>{}, total, std::false_type{});
   };
   if (c2 >= 0.0f)
     body(std::false_type{});
