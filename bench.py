@@ -43,7 +43,7 @@ def parse():
                     help="budget of the cpu_baseline sample (0 disables it)")
     ap.add_argument("--workload", default="C2", choices=["C2", "C3", "C4", "C5"],
                     help="C2 is the headline; C3-C5 are the other BASELINE.json configurations, "
-                         "timed the same way (no cpu_baseline, no committed traffic figure)")
+                         "timed the same way (no cpu_baseline)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="before the timed steps, run plain device copies of this many MiB "
                          "(the byte-count calibration for rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -95,13 +95,23 @@ def make_workload(cfg, dev, torch):
     return a.contiguous(), b.contiguous(), cfg.logit_scale, scale_a, scale_b
 
 
-def load_traffic():
-    p = ROOT / "profiles" / "c2_f16_exchange_traffic.json"
-    if not p.exists():
+# the path each committed traffic summary was measured on (what "auto" picks)
+PROFILED_PATH = {"C2": "exchange", "C3": "rows", "C4": "split", "C5": "split"}
+
+
+def load_traffic(workload: str = "C2", path: str = "auto"):
+    """HBM bytes per launch of the workload's dominant kernel, from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summaries (None if absent, or if this run
+    takes another path than the one profiled)."""
+    if path not in ("auto", PROFILED_PATH.get(workload)):
         return None
     try:
-        return json.loads(p.read_text()).get("hbm_bytes_per_launch")
-    except (OSError, ValueError):
+        if workload == "C2":
+            p = ROOT / "profiles" / "c2_f16_exchange_traffic.json"
+            return json.loads(p.read_text()).get("hbm_bytes_per_launch")
+        p = ROOT / "profiles" / "c3_c4_c5_traffic.json"
+        return json.loads(p.read_text())["workloads"][workload]["hbm_bytes_per_launch"]
+    except (OSError, ValueError, KeyError):
         return None
 
 
@@ -186,10 +196,12 @@ def main():
             "config": {"workload": cfg.name, "batch": cfg.batch, "m": m, "n": n, "k": k,
                        "in_dtype": cfg.in_dtype, "out_dtype": cfg.out_dtype, "path": args.path},
             "roofline": ({"bound": "mfma", "achieved": round(tflops, 3), "peak": peak,
-                          "unit": "TFLOP/s", "frac": round(tflops / peak, 4), "traffic": None}
+                          "unit": "TFLOP/s", "frac": round(tflops / peak, 4),
+                          "traffic": load_traffic(args.workload, args.path)}
                          if mfma_bound else
                          {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
-                          "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None}),
+                          "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
+                          "traffic": load_traffic(args.workload, args.path)}),
             "checks": {"row_sum_max_dev": row_dev, "device_error_flags": flags},
         }
         print(json.dumps(line), flush=True)
@@ -213,7 +225,7 @@ def main():
                    "batch": 1, "accumulate": "f32", "out_dtype": "f16", "path": args.path},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 3), "peak": PEAK_F16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tflops / PEAK_F16_TFLOPS, 4),
-                     "traffic": load_traffic()},
+                     "traffic": load_traffic("C2", args.path)},
         "cpu_baseline": cpu,
         "checks": {"row_sum_max_dev": row_dev, "device_error_flags": flags,
                    "host_wall_s_timed_region": round(t_host, 4)},
