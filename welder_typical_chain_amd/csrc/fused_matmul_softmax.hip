@@ -814,10 +814,13 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
     }
     return make_float2(tm, ts);
   };
+  // A row block of a single column tile (N <= 128) needs no exchange: the
+  // tile's own statistics are the row's.
+  const bool solo = EPI == kEpiExchange && nT32 == 1u;
   if constexpr (EPI != kEpiLogits) {
     __syncthreads();  // the wave statistics are in place
     // Publish this tile's row statistics (partial[row block][row][column tile]).
-    if (t < BM) {
+    if (t < BM && !solo) {
       const float2 st = tile_stat(t);
       store_stat(p.partial + ((int64_t)rbg * BM + t) * p.nT + nt, st.x, st.y);
     }
@@ -842,9 +845,11 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
 
   if constexpr (EPI != kEpiLogits) {
     if constexpr (EPI == kEpiExchange) {
-      if (t < BM) __builtin_amdgcn_s_waitcnt(0);  // statistics stores complete before this tile is counted
-      __syncthreads();
-      if (t == 0) rowblock_barrier(p.sync + kSyncWords * rbg, gen0, p.nT, p.err, p.spin_ticks);
+      if (!solo) {
+        if (t < BM) __builtin_amdgcn_s_waitcnt(0);  // statistics stores complete before this tile is counted
+        __syncthreads();
+        if (t == 0) rowblock_barrier(p.sync + kSyncWords * rbg, gen0, p.nT, p.err, p.spin_ticks);
+      }
     }
     constexpr int P = NT / BM;  // threads per row (== WN)
     static_assert(P == WN, "one thread per (row, wave column slice)");
@@ -855,10 +860,15 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
       // pairs, loaded straight from the workspace in batches of 8
       // independent loads, then combine with their partner lanes.
       const int part = (p.nT + P - 1) / P;
-      const int q0 = h * part < p.nT ? h * part : p.nT;
-      const int q1 = q0 + part < p.nT ? q0 + part : p.nT;
+      const int q0 = solo ? 0 : (h * part < p.nT ? h * part : p.nT);
+      const int q1 = solo ? 0 : (q0 + part < p.nT ? q0 + part : p.nT);
       const float2* st = p.partial + ((int64_t)rbg * BM + r) * p.nT;
       float gm = -INFINITY, gs = 0.0f;
+      if (solo && h == 0) {  // the row's statistics from this tile's wave entries in LDS
+        const float2 ts = tile_stat(r);
+        gm = ts.x;
+        gs = ts.y;
+      }
       for (int qb = q0; qb < q1; qb += 8) {
         float2 v[8];
 #pragma unroll
