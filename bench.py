@@ -142,9 +142,22 @@ def main():
     out_code = {"f32": _lib.DTYPE_F32, "f16": _lib.DTYPE_F16, "bf16": _lib.DTYPE_BF16}[cfg.out_dtype]
     ws = new_workspace(workspace_size(cfg.batch, m, n, k, in_code, out_code, args.path), dev)
 
+    # One step = one call of the launcher C-ABI (the drop-in boundary), with
+    # its arguments marshalled once: the torch wrapper's own host work (about
+    # 5 us per call) would otherwise be timed too, and for short calls it,
+    # not the GPU, sets the pace.  The first call goes through the wrapper,
+    # which checks shapes and dtypes.
+    matmul_softmax(a, b, out=out, path=args.path, workspace=ws, logit_scale=logit_scale,
+                   scale_a=scale_a, scale_b=scale_b)
+    launch = _lib.lib().wtc_matmul_softmax
+    call_args = (a.data_ptr(), b.data_ptr(), out.data_ptr(), cfg.batch, m, n, k, in_code, out_code,
+                 float(logit_scale), float(scale_a), float(scale_b), _lib.PATHS[args.path],
+                 ws.data_ptr(), ws.numel(), torch.cuda.current_stream(dev).cuda_stream)
+
     def step():
-        matmul_softmax(a, b, out=out, path=args.path, workspace=ws, logit_scale=logit_scale,
-                       scale_a=scale_a, scale_b=scale_b)
+        rc = launch(*call_args)
+        if rc:
+            _lib.check(rc)
 
     if args.copy_probe_mib > 0:
         n_el = args.copy_probe_mib * (1 << 20) // 4

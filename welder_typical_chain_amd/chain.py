@@ -86,12 +86,16 @@ def matmul_softmax(a: torch.Tensor, b: torch.Tensor, *, out: torch.Tensor | None
     if workspace is not None:
         ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
     stream = torch.cuda.current_stream(a.device).cuda_stream
-    with torch.cuda.device(a.device):
-        rc = _lib.lib().wtc_matmul_softmax(
-            a.data_ptr(), b.data_ptr(), out.data_ptr(), batch, m, n, k, in_code, out_code,
+    call = (a.data_ptr(), b.data_ptr(), out.data_ptr(), batch, m, n, k, in_code, out_code,
             float(logit_scale), float(scale_a), float(scale_b), _lib.PATHS[path], ws_ptr,
             ws_bytes, stream)
-    _lib.check(rc)
+    if a.device.index == torch.cuda.current_device():
+        rc = _lib.lib().wtc_matmul_softmax(*call)
+    else:  # the library launches on the current device
+        with torch.cuda.device(a.device):
+            rc = _lib.lib().wtc_matmul_softmax(*call)
+    if rc:
+        _lib.check(rc)
     return out
 
 
