@@ -78,6 +78,34 @@ def test_ragged_shapes(native_lib, in_dtype, out_dtype, path):
 
 
 @needs_gpu
+@pytest.mark.parametrize("in_dtype,out_dtype", [("f16", "f16"), ("bf16", "bf16"), ("f16", "f32"),
+                                                ("fp8", "f16"), ("f32", "f32"), ("bf16", "f16")])
+@pytest.mark.parametrize("n", [128, 72])
+def test_exchange_single_column_tile(native_lib, in_dtype, out_dtype, n):
+    """N <= 128: one column tile per row block, normalised from the tile's own
+    statistics without the cross-workgroup exchange (ragged M and K too), and
+    the row-block counters are left untouched for the next call."""
+    from welder_typical_chain_amd.chain import new_workspace, read_diagnostics, workspace_size
+    m = 300
+    k = {"f16": 72, "bf16": 72, "f32": 36, "fp8": 80}[in_dtype]
+    dist = "xorshift_uniform" if in_dtype == "f32" else "normal"
+    cfg = ChainConfig("solo", 1, m, n, k, in_dtype, out_dtype, dist, 0.3)
+    _announce(f"single column tile {in_dtype}->{out_dtype} {m}x{n}x{k} path=exchange")
+    codes = {"f32": 0, "f16": 1, "bf16": 2, "fp8": 3}
+    ws = new_workspace(workspace_size(1, 2048, 2048, 1024, codes[in_dtype], codes[out_dtype]))
+    inp = O.make_inputs(cfg, seed=9)
+    out = run_chain(inp, in_dtype, out_dtype, path="exchange", workspace=ws)
+    _check(cfg, inp, out, np.arange(m))
+    # the same workspace then serves a multi-tile exchange call correctly
+    cfg2 = ChainConfig("after-solo", 1, 256, 384, k, in_dtype, out_dtype, dist, 0.3)
+    inp2 = O.make_inputs(cfg2, seed=10)
+    out2 = run_chain(inp2, in_dtype, out_dtype, path="exchange", workspace=ws)
+    _check(cfg2, inp2, out2, np.arange(256))
+    flags, _, timeouts = read_diagnostics(ws)
+    assert flags == 0 and timeouts == 0
+
+
+@needs_gpu
 @pytest.mark.parametrize("in_dtype,out_dtype", [("f16", "f16"), ("bf16", "f32"), ("fp8", "f16"),
                                                 ("bf16", "bf16")])
 def test_split_256_row_tiles_ragged(native_lib, in_dtype, out_dtype):
