@@ -13,7 +13,9 @@ Prints ONE JSON line.  `roofline` prices the kernel against dense f16 MFMA
 peak (2.5 PFLOP/s); `traffic` comes from the committed rocprofv3 --pmc
 summary of this same command (profiles/), or is null.  `cpu_baseline` times
 the chain lowered to f32 loops (oracle/, the restatement of the reference's
-mlir-opt CPU path) on a bounded sample of rows on this host.
+mlir-opt CPU path) on a bounded sample of rows on this host.  `launch`
+gives the single-launch figures: one call's GPU time on an idle stream, its
+excess over the back-to-back time per call, and the host enqueue cost.
 """
 from __future__ import annotations
 
@@ -182,6 +184,31 @@ def main():
     torch.cuda.synchronize()
     t_host = time.perf_counter() - t_host0
     ms = e0.elapsed_time(e1) / args.steps
+
+    # Single-launch figures, outside the timed region: the GPU time of one
+    # call on an idle stream (events around it), its excess over the
+    # back-to-back time per call (launch overhead), and the host's cost to
+    # enqueue one call.
+    single = []
+    for _ in range(20):
+        torch.cuda.synchronize()
+        s0 = torch.cuda.Event(enable_timing=True)
+        s1 = torch.cuda.Event(enable_timing=True)
+        s0.record(stream)
+        step()
+        s1.record(stream)
+        s1.synchronize()
+        single.append(s0.elapsed_time(s1) * 1e3)
+    single_us = sorted(single)[len(single) // 2]
+    torch.cuda.synchronize()
+    h0 = time.perf_counter()
+    for _ in range(50):
+        step()
+    enqueue_us = (time.perf_counter() - h0) / 50 * 1e6
+    torch.cuda.synchronize()
+    launch_info = {"single_call_us": round(single_us, 2), "back_to_back_us": round(ms * 1e3, 2),
+                   "launch_overhead_us": round(single_us - ms * 1e3, 2),
+                   "host_enqueue_us": round(enqueue_us, 2)}
     flops = cfg.flops
     tflops = flops / (ms * 1e-3) / 1e12
     from welder_typical_chain_amd.chain import read_error_flags
@@ -215,6 +242,7 @@ def main():
                          {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
                           "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
                           "traffic": load_traffic(args.workload, args.path)}),
+            "launch": launch_info,
             "checks": {"row_sum_max_dev": row_dev, "device_error_flags": flags},
         }
         print(json.dumps(line), flush=True)
@@ -240,6 +268,7 @@ def main():
                      "unit": "TFLOP/s", "frac": round(tflops / PEAK_F16_TFLOPS, 4),
                      "traffic": load_traffic("C2", args.path)},
         "cpu_baseline": cpu,
+        "launch": launch_info,
         "checks": {"row_sum_max_dev": row_dev, "device_error_flags": flags,
                    "host_wall_s_timed_region": round(t_host, 4)},
     }
