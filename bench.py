@@ -62,9 +62,15 @@ def cpu_baseline(a_host, b_host, n, k, budget_s):
     rows = min(rows, a_host.shape[0])
     _, secs = O.cpu_chain_loops(a_host, b_host, 0, rows, threads)
     tflops = 2.0 * rows * n * k / secs / 1e12
+    # the same loops on one core (the loops lowering runs single-threaded),
+    # on a smaller sample: about a quarter of the budget, at least 8 rows
+    rows1 = min(a_host.shape[0], max(8, int(budget_s / 4 / per_row)))
+    _, secs1 = O.cpu_chain_loops(a_host, b_host, 0, rows1, 1)
     return {"value": tflops, "unit": "TFLOP/s", "cores": threads, "kind": "port",
             "sample": f"{rows} of 2048 rows of C2 (f32 i-j-k loops + max/exp/sum/div, "
-                      f"OpenMP over rows), {secs:.1f} s"}
+                      f"OpenMP over rows), {secs:.1f} s",
+            "single_thread": {"value": 2.0 * rows1 * n * k / secs1 / 1e12, "cores": 1,
+                              "sample": f"{rows1} rows, {secs1:.1f} s"}}
 
 
 PEAKS = {"f16": PEAK_F16_TFLOPS, "bf16": PEAK_F16_TFLOPS, "fp8": 5000.0}
