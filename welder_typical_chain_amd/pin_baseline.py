@@ -48,7 +48,10 @@ def pin(run_args, baseline_dir: Path) -> dict:
         for name in VARIANT_FILES:
             shutil.copyfile(run_base / variant / name, baseline_dir / variant / name)
     import torch
-    device = torch.cuda.get_device_name(0) if torch.cuda.is_available() else "none"
+    device = "none"
+    if torch.cuda.is_available():
+        props = torch.cuda.get_device_properties(0)
+        device = f"{props.name} ({props.gcnArchName}, {props.multi_processor_count} CUs)"
     input_mlir = run_args.input_mlir or str(run_base / "input.mlir")
     manifest = [
         f"timestamp={datetime.datetime.now().astimezone().isoformat(timespec='seconds')}",
