@@ -19,7 +19,10 @@
  *
  * Thread safety: calls on one device that share a workspace (including the
  * default one) must not overlap; pass distinct workspaces to run calls
- * concurrently on several streams.
+ * concurrently on several streams.  Two EXCHANGE-path calls must not run
+ * concurrently on one device: each needs all of its tiles co-resident, so
+ * each may hold CUs that the other's row blocks wait for (the wait is
+ * bounded; it ends with an error flag, see wtc_read_error_flags).
  */
 #ifndef WTC_HIP_H
 #define WTC_HIP_H

@@ -310,3 +310,50 @@ def test_graph_replay_matches_eager(native_lib, path, shape, in_dt):
         torch.cuda.synchronize()
         assert torch.equal(out, ref), f"replay {rep}: max diff {(out.float() - ref.float()).abs().max().item()}"
         del junk
+
+
+@needs_gpu
+def test_concurrent_host_threads_on_streams(native_lib):
+    """Four host threads, each with its own stream and workspace, call the
+    launcher concurrently (the C-ABI call releases the GIL, so the calls
+    meet in the library's launch code) on the split, row-block and unfused
+    paths; every result must match the torch fp32 reference of its inputs."""
+    import threading
+    from welder_typical_chain_amd.chain import matmul_softmax, new_workspace, workspace_size
+    _announce("4 host threads x 12 calls, own streams and workspaces (split/rows/unfused)")
+    dev = torch.device("cuda")
+    jobs = [("split", 640, 1000, 256), ("rows", 512, 1024, 128), ("unfused", 300, 520, 64),
+            ("split", 256, 4096, 128)]
+    errors, worst = [], [0.0] * len(jobs)
+
+    def work(i, path, m, n, k):
+        try:
+            stream = torch.cuda.Stream(device=dev)
+            g = torch.Generator(device=dev)
+            g.manual_seed(100 + i)
+            with torch.cuda.stream(stream):
+                ws = new_workspace(workspace_size(1, m, n, k, 1, 1, path), dev)
+                for it in range(12):
+                    a = (torch.randn((m, k), generator=g, device=dev) / k ** 0.5).half()
+                    b = (torch.randn((k, n), generator=g, device=dev) * (1 + it / 6)).half()
+                    out = matmul_softmax(a, b, out_dtype=torch.float16, path=path, workspace=ws)
+                    ref = torch.softmax(a.float() @ b.float(), dim=-1)
+                    d = (out.float() - ref).abs()
+                    bad = d > 2e-3 + 1e-2 * ref
+                    worst[i] = max(worst[i], float(d.max()))
+                    if bool(bad.any()):
+                        errors.append(f"thread {i} ({path}) call {it}: max abs {float(d.max()):.3e}")
+                        return
+            stream.synchronize()
+        except Exception as e:  # reported below, on the main thread
+            errors.append(f"thread {i} ({path}): {e!r}")
+
+    threads = [threading.Thread(target=work, args=(i, *j)) for i, j in enumerate(jobs)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=120)
+    assert not any(t.is_alive() for t in threads), "a worker thread did not finish"
+    torch.cuda.synchronize()
+    print(f"[gpu-case] worst abs err per thread {['%.2e' % w for w in worst]}")
+    assert not errors, errors
