@@ -15,7 +15,9 @@ summary of this same command (profiles/), or is null.  `cpu_baseline` times
 the chain lowered to f32 loops (oracle/, the restatement of the reference's
 mlir-opt CPU path) on a bounded sample of rows on this host.  `launch`
 gives the single-launch figures: one call's GPU time on an idle stream, its
-excess over the back-to-back time per call, and the host enqueue cost.
+difference from the back-to-back time per call (the launch overhead for short
+calls; negative for long ones, which run at a higher clock when alone), and
+the host enqueue cost.
 """
 from __future__ import annotations
 
@@ -192,9 +194,11 @@ def main():
     ms = e0.elapsed_time(e1) / args.steps
 
     # Single-launch figures, outside the timed region: the GPU time of one
-    # call on an idle stream (events around it), its excess over the
-    # back-to-back time per call (launch overhead), and the host's cost to
-    # enqueue one call.
+    # call on an idle stream (events around it), its difference from the
+    # back-to-back time per call, and the host's cost to enqueue one call.
+    # The difference is the launch overhead for short calls; long calls
+    # measured alone run at a higher clock than a sustained stream of them,
+    # which makes it negative.
     single = []
     for _ in range(20):
         torch.cuda.synchronize()
@@ -213,7 +217,7 @@ def main():
     enqueue_us = (time.perf_counter() - h0) / 50 * 1e6
     torch.cuda.synchronize()
     launch_info = {"single_call_us": round(single_us, 2), "back_to_back_us": round(ms * 1e3, 2),
-                   "launch_overhead_us": round(single_us - ms * 1e3, 2),
+                   "single_minus_back_to_back_us": round(single_us - ms * 1e3, 2),
                    "host_enqueue_us": round(enqueue_us, 2)}
     flops = cfg.flops
     tflops = flops / (ms * 1e-3) / 1e12
