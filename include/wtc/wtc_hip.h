@@ -9,7 +9,10 @@
  * cuLaunchKernel (backend/welder/compiler/solver/WelderProfiler.cpp:752-792).
  * A HIP code object has no such text form, so the launch is a C call taking
  * device pointers.  All buffers are owned by the caller; the library owns
- * only a per-device default workspace (used when `workspace` is NULL).
+ * only the default workspaces (one per stream that passed a NULL
+ * `workspace`; they grow when a larger problem needs it and are never freed
+ * before the process ends, since a captured graph may hold their address) and
+ * one pinned host word per device (the timeout mailbox).
  *
  * Layouts are dense row-major: A [batch][m][k], B [batch][k][n],
  * out [batch][m][n] (the reference's strides [K,1] / [N,1] / [N,1],
@@ -17,12 +20,17 @@
  * must be a multiple of 16 and n a multiple of 8.  m, n, batch may be 0
  * (nothing to do); k may be 0 (every row is uniform 1/n).
  *
- * Thread safety: calls on one device that share a workspace (including the
- * default one) must not overlap; pass distinct workspaces to run calls
- * concurrently on several streams.  Two EXCHANGE-path calls must not run
- * concurrently on one device: each needs all of its tiles co-resident, so
- * each may hold CUs that the other's row blocks wait for (the wait is
- * bounded; it ends with an error flag, see wtc_read_error_flags).
+ * Thread safety: calls may come from any host thread.  Calls that share a
+ * caller workspace must not overlap on the GPU (the default workspaces are
+ * per stream, so NULL-workspace calls on different streams never share one).
+ * An EXCHANGE-path call needs all of its tiles resident at once: the library
+ * orders the exchange calls it makes on different streams of one device (an
+ * event recorded after each, waited for by the next on another stream;
+ * not for streams being captured into a graph).  If other work -- another
+ * process, or a replayed graph -- holds the CUs its tiles wait for, the wait
+ * ends after a bounded time and the call's output is wrong: that is reported
+ * as WTC_ERR_TIMEOUT by the next wtc_matmul_softmax or wtc_check_status on
+ * the device (see also wtc_read_error_flags).
  */
 #ifndef WTC_HIP_H
 #define WTC_HIP_H
@@ -40,6 +48,9 @@ extern "C" {
 #define WTC_ERR_WORKSPACE 2    /* caller workspace too small */
 #define WTC_ERR_HIP 3          /* a HIP runtime call failed */
 #define WTC_ERR_UNSUPPORTED 4  /* shape / path combination not available */
+#define WTC_ERR_TIMEOUT 5      /* an earlier exchange-path call on this device timed out
+                                  waiting for its tiles; its output is wrong (reported
+                                  once; the call that reports it does nothing else) */
 
 /* Element types. */
 #define WTC_DTYPE_F32 0
@@ -88,11 +99,21 @@ int wtc_plan(int64_t batch, int64_t m, int64_t n, int64_t k, int in_dtype,
              int64_t *grid, int *chosen_path, int64_t *workspace_bytes);
 
 /* Reads (and with clear != 0, resets) the three diagnostic words of a
- * workspace (NULL = the default workspace of the current device) into
- * flags[0..2]: flags[0] bit 0 = a row-block wait of the exchange path timed
- * out, flags[1] = longest row-block wait in 100 MHz ticks, flags[2] = number
- * of timed-out waits.  Synchronises the device. */
+ * workspace (NULL = all default workspaces of the current device, or-ed /
+ * max-ed / summed) into flags[0..2]: flags[0] bit 0 = an exchange-path wait
+ * timed out, flags[1] = longest exchange-path wait in 100 MHz ticks,
+ * flags[2] = number of timed-out waits.  Synchronises the device. */
 int wtc_read_error_flags(void *workspace, uint32_t *flags, int clear);
+
+/* Synchronises `stream` (a hipStream_t, NULL = the null stream) and returns
+ * WTC_ERR_TIMEOUT if an exchange-path wait of any call on the current device
+ * timed out since the last report, else WTC_OK. */
+int wtc_check_status(void *stream);
+
+/* Limit of every exchange-path wait, in ticks of the 100 MHz real-time clock
+ * (0 = the default, 2 s).  Applies to calls made after it; for tests of the
+ * timeout reporting. */
+int wtc_set_exchange_wait_limit(uint64_t ticks);
 
 /* Message of the last failing call on this thread ("" if none). */
 const char *wtc_last_error(void);

@@ -145,6 +145,71 @@ def test_c3_batched_attention(native_lib, path):
 
 
 @needs_gpu
+def test_c3_full_batch(native_lib):
+    """C3 at its configured size: 64 batch x heads of 2048 x 2048 x 128, scale
+    1/sqrt(128), through auto (the row-block path: 1024 row blocks, four per
+    CU).  Sampled rows of batches 0, 31 and 63 against the oracle; the row
+    sums of all 131072 rows on the GPU."""
+    cfg = CONFIGS["C3"]
+    _announce("C3 f16 batched 64x2048x2048x128 (full size) path=auto")
+    inp = O.make_inputs(cfg, seed=0)
+    assert inp.a.shape[0] == 64
+    out = run_chain(inp, cfg.in_dtype, cfg.out_dtype, path="auto", batched=True)
+    rows = sample_rows(cfg.m, 12)
+    for bt in (0, 31, 63):
+        logits, probs = O.chain_rows(inp.a[bt], inp.b[bt], rows, inp.scale)
+        got = out[bt][torch.from_numpy(rows).to(out.device)].float().cpu().numpy()
+        compare_rows(got, probs, logits, cfg.out_dtype, label=f"C3 batch {bt}", in_dtype=cfg.in_dtype)
+    worst = 0.0
+    for bt in range(0, 64, 8):  # row sums in chunks of 8 batches (16 Mi entries each)
+        s = out[bt:bt + 8].float().sum(-1)
+        worst = max(worst, float((s - 1.0).abs().max()))
+        assert bool(torch.isfinite(out[bt:bt + 8]).all())
+    print(f"[gpu-case] C3 full: max row-sum deviation {worst:.2e} over 131072 rows")
+    assert worst <= 1e-3
+
+
+@needs_gpu
+def test_exchange_calls_on_two_streams(native_lib):
+    """Exchange-path calls alternating between two streams with their own
+    workspaces: the library orders them (each needs all of its tiles
+    resident), so every result matches the fp32 reference and no wait times
+    out."""
+    import math
+    from welder_typical_chain_amd.chain import (check_status, matmul_softmax, new_workspace,
+                                                read_diagnostics, workspace_size)
+    _announce("exchange calls alternating between two streams, 2 x 12 calls")
+    dev = torch.device("cuda")
+    m = n = 2048
+    k = 512
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    wss = [new_workspace(workspace_size(1, m, n, k, 1, 1, "exchange"), dev) for _ in streams]
+    g = torch.Generator(device=dev)
+    g.manual_seed(21)
+    jobs = []
+    for it in range(24):
+        a = (torch.randn((m, k), generator=g, device=dev) / math.sqrt(k)).half()
+        b = (torch.randn((k, n), generator=g, device=dev) * (1 + it / 12)).half()
+        jobs.append((a, b))
+    torch.cuda.synchronize()
+    outs = []
+    for it, (a, b) in enumerate(jobs):
+        i = it % 2
+        streams[i].wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(streams[i]):
+            outs.append(matmul_softmax(a, b, path="exchange", workspace=wss[i]))
+    torch.cuda.synchronize()
+    check_status()
+    worst = 0.0
+    for (a, b), out in zip(jobs, outs):
+        ref = torch.softmax(a.float() @ b.float(), dim=-1)
+        worst = max(worst, float((out.float() - ref).abs().max()))
+    flags = [read_diagnostics(w) for w in wss]
+    print(f"[gpu-case] worst abs err {worst:.2e}; diagnostics {flags}")
+    assert worst < 2e-3 and all(f[0] == 0 and f[2] == 0 for f in flags)
+
+
+@needs_gpu
 @pytest.mark.parametrize("in_dtype,out_dtype", [("f16", "f16"), ("bf16", "bf16"), ("f16", "f32"),
                                                 ("bf16", "f16")])
 @pytest.mark.parametrize("m,n,k", [(200, 264, 72), (128, 128, 128), (64, 4104, 8), (300, 136, 120)])

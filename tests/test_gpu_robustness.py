@@ -1,0 +1,132 @@
+"""GPU tests of the launcher's failure reporting and default workspaces.
+
+* A timed-out exchange wait reaches the caller: the wait limit is set to a
+  few ticks from the host, so the first tiles of every row block give up
+  (every kernel still exits normally: all waits are bounded), and the error
+  must come back as WTC_ERR_TIMEOUT from wtc_check_status and from the next
+  call, once.
+* Default workspaces: one per stream, grow-only; none is allocated while the
+  stream is being captured; a graph captured with the default workspace still
+  replays correctly after an eager call of a larger shape grew it.
+"""
+from __future__ import annotations
+
+import math
+
+import pytest
+
+torch = pytest.importorskip("torch")
+
+pytestmark = pytest.mark.gpu
+
+needs_gpu = pytest.mark.skipif(not torch.cuda.is_available(), reason="no GPU")
+
+
+def _announce(msg: str) -> None:
+    print(f"\n[gpu-case] {msg}", flush=True)
+
+
+def _inputs(m, n, k, seed, dev="cuda"):
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    a = (torch.randn((m, k), generator=g, device=dev) / math.sqrt(k)).half()
+    b = torch.randn((k, n), generator=g, device=dev).half()
+    return a, b
+
+
+@needs_gpu
+def test_exchange_timeout_is_reported(native_lib):
+    from welder_typical_chain_amd import _lib
+    from welder_typical_chain_amd.chain import (check_status, matmul_softmax, new_workspace,
+                                                read_diagnostics, set_exchange_wait_limit,
+                                                workspace_size)
+    _announce("exchange wait limit of 2 ticks: timeouts reported, then a clean call")
+    m = n = 2048
+    k = 256
+    a, b = _inputs(m, n, k, 3)
+    ws = new_workspace(workspace_size(1, m, n, k, 1, 1, "exchange"))
+    ref = torch.softmax(a.float() @ b.float(), dim=-1)
+    try:
+        set_exchange_wait_limit(2)  # 20 ns: tiles that finish first give up
+        reported = False
+        for _ in range(3):
+            matmul_softmax(a, b, path="exchange", workspace=ws)
+            try:
+                check_status()
+            except _lib.WtcError as e:
+                assert e.code == _lib.WTC_ERR_TIMEOUT, e
+                reported = True
+                break
+        flags, _, timeouts = read_diagnostics(ws)
+        print(f"[gpu-case] reported {reported}; workspace flags {flags} timeouts {timeouts}")
+        assert reported and flags & 1 and timeouts > 0
+        # reported once: the status is clean now
+        check_status()
+        # a timeout left in the mailbox is reported by the next call, which does nothing else
+        matmul_softmax(a, b, path="exchange", workspace=ws)
+        torch.cuda.synchronize()
+        with pytest.raises(_lib.WtcError) as ei:
+            matmul_softmax(a, b, path="exchange", workspace=ws)
+        assert ei.value.code == _lib.WTC_ERR_TIMEOUT
+    finally:
+        set_exchange_wait_limit(0)
+    read_diagnostics(ws)  # clear the workspace's words
+    out = matmul_softmax(a, b, path="exchange", workspace=ws, check=True)
+    err = float((out.float() - ref).abs().max())
+    flags, longest, timeouts = read_diagnostics(ws)
+    print(f"[gpu-case] clean call: max abs err {err:.2e}, longest wait {longest / 100:.1f} us")
+    assert err < 2e-3 and flags == 0 and timeouts == 0
+
+
+@needs_gpu
+def test_default_workspace_not_allocated_during_capture(native_lib):
+    from welder_typical_chain_amd import _lib
+    from welder_typical_chain_amd.chain import matmul_softmax
+    _announce("NULL workspace on a capturing stream without a default workspace is refused")
+    a, b = _inputs(256, 512, 64, 5)
+    s = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    raised = None
+    with torch.cuda.graph(graph, stream=s):
+        try:
+            matmul_softmax(a, b, path="exchange")
+        except _lib.WtcError as e:
+            raised = e
+    torch.cuda.synchronize()
+    assert raised is not None and raised.code == _lib.WTC_ERR_ARG, raised
+    assert "captur" in str(raised)
+
+
+@needs_gpu
+def test_graph_with_default_workspace_survives_its_growth(native_lib):
+    """A graph captured with the stream's default workspace; then an eager
+    call of a larger shape on the same stream grows that workspace; every
+    replay of the graph must still match the eager output bit for bit (the
+    superseded buffer stays allocated)."""
+    from welder_typical_chain_amd.chain import matmul_softmax
+    _announce("graph on the default workspace, then the workspace grows, then replays")
+    a, b = _inputs(512, 1024, 128, 7)
+    big_a, big_b = _inputs(2048, 8192, 128, 8)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    out = torch.empty((512, 1024), dtype=torch.float16, device="cuda")
+    with torch.cuda.stream(s):
+        for _ in range(2):  # creates the stream's default workspace outside the capture
+            matmul_softmax(a, b, out=out, path="split")
+    torch.cuda.synchronize()
+    ref = out.clone()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        matmul_softmax(a, b, out=out, path="split")
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s):
+        big = matmul_softmax(big_a, big_b, path="split")  # needs a larger default workspace
+    torch.cuda.synchronize()
+    big_ref = torch.softmax(big_a[:64].float() @ big_b.float(), dim=-1)
+    assert float((big[:64].float() - big_ref).abs().max()) < 2e-3
+    for rep in range(3):
+        out.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), f"replay {rep}"

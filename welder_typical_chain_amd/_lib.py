@@ -15,6 +15,7 @@ WTC_ERR_ARG = 1
 WTC_ERR_WORKSPACE = 2
 WTC_ERR_HIP = 3
 WTC_ERR_UNSUPPORTED = 4
+WTC_ERR_TIMEOUT = 5
 
 DTYPE_F32 = 0
 DTYPE_F16 = 1
@@ -47,6 +48,8 @@ SIGNATURES = {
                                 ctypes.POINTER(_c_i64), ctypes.POINTER(ctypes.c_int),
                                 ctypes.POINTER(_c_i64)]),
     "wtc_read_error_flags": (ctypes.c_int, [_c_p, ctypes.POINTER(ctypes.c_uint32), ctypes.c_int]),
+    "wtc_check_status": (ctypes.c_int, [_c_p]),
+    "wtc_set_exchange_wait_limit": (ctypes.c_int, [ctypes.c_uint64]),
     "wtc_last_error": (ctypes.c_char_p, []),
     "wtc_version": (ctypes.c_char_p, []),
     "welder_compile_typical_chain_to_nvvm": (ctypes.c_int, [

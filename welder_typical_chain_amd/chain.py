@@ -51,12 +51,15 @@ def new_workspace(nbytes: int, device: torch.device | str = "cuda") -> torch.Ten
 def matmul_softmax(a: torch.Tensor, b: torch.Tensor, *, out: torch.Tensor | None = None,
                    out_dtype: torch.dtype | None = None, logit_scale: float = 1.0,
                    scale_a: float = 1.0, scale_b: float = 1.0, path: str = "auto",
-                   workspace: torch.Tensor | None = None) -> torch.Tensor:
+                   workspace: torch.Tensor | None = None, check: bool = False) -> torch.Tensor:
     """out = softmax_row(logit_scale * scale_a * scale_b * (a @ b)).
 
     a: [M, K] or [batch, M, K]; b: [K, N] or [batch, K, N]; contiguous CUDA
     tensors of float32 / float16 / bfloat16 / float8_e4m3fn (or uint8 holding
-    e4m3 bytes).  Runs on the current stream of a's device.
+    e4m3 bytes).  Runs on the current stream of a's device.  With check=True
+    the stream is synchronised afterwards and a timed-out exchange wait
+    raises WtcError (code WTC_ERR_TIMEOUT) instead of being reported by the
+    next call.
     """
     if a.dim() not in (2, 3) or b.dim() != a.dim():
         raise ValueError("a and b must both be 2-D or both 3-D")
@@ -96,16 +99,34 @@ def matmul_softmax(a: torch.Tensor, b: torch.Tensor, *, out: torch.Tensor | None
             rc = _lib.lib().wtc_matmul_softmax(*call)
     if rc:
         _lib.check(rc)
+    if check:
+        check_status(a.device)
     return out
 
 
+def check_status(device: torch.device | str | None = None) -> None:
+    """Synchronise the current stream of `device` and raise WtcError if an
+    exchange-path wait of any call on the device timed out since the last
+    report (wtc_check_status)."""
+    dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+    with torch.cuda.device(dev):
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        _lib.check(_lib.lib().wtc_check_status(stream))
+
+
+def set_exchange_wait_limit(ticks: int) -> None:
+    """Limit of each exchange-path wait in 100 MHz ticks (0 = default, 2 s)."""
+    _lib.check(_lib.lib().wtc_set_exchange_wait_limit(int(ticks)))
+
+
 def read_error_flags(workspace: torch.Tensor | None = None, clear: bool = True) -> int:
-    """Bit 0 set when a row-block wait of the exchange path timed out."""
+    """Bit 0 set when an exchange-path wait timed out."""
     return read_diagnostics(workspace, clear)[0]
 
 
 def read_diagnostics(workspace: torch.Tensor | None = None, clear: bool = True):
-    """(flags, longest row-block wait in 100 MHz ticks, timed-out waits)."""
+    """(flags, longest exchange wait in 100 MHz ticks, timed-out waits) of a
+    workspace, or of all default workspaces of the current device."""
     import ctypes
     words = (ctypes.c_uint32 * 3)()
     ptr = workspace.data_ptr() if workspace is not None else None

@@ -62,15 +62,30 @@ constexpr int STAGE_BYTES = A_STAGE_BYTES + BN * kKTileBytes;    // 32 KiB
 // keeps k-tiles kt+1 .. kt+3 in flight or landed while k-tile kt's fragments
 // are in registers, so 3 stages suffice when a stage may be refilled as soon
 // as its fragments have been read.
-template <int IN_DT, int TM = 128> struct Cfg {
+//
+// KS = 2 (k-split, 128-row tiles of 16-bit and fp8 inputs): the 8 waves form
+// 2 x 2 x 2 (M x N x K); the two waves of a (M, N) pair each own the same
+// 64x64 block and run half of every k-tile's MFMA k-steps, so each wave reads
+// 64 A rows and 64 B columns per k-step instead of 64 and 32 -- a third less
+// LDS read traffic per MFMA than 64x32 blocks.  After the K loop each wave
+// hands the partner its partial sums of one 32-column half and adds the
+// partner's of the other (one LDS round trip), leaving every wave a 64x32
+// block, which is the epilogue's layout for KS = 1 as well.
+template <int IN_DT, int TM = 128, int KS = 1> struct Cfg {
   static constexpr bool kDma = IN_DT == DT_F16 || IN_DT == DT_BF16 || IN_DT == DT_FP8;
   static_assert(TM == 128 || (TM == 256 && kDma), "tile height");
+  static_assert(KS == 1 || (KS == 2 && kDma && TM == 128), "k-split layout");
   static constexpr int kBM = TM;
+  static constexpr int kKS = KS;
   static constexpr int kWavesM = kDma ? TM / 64 : 2;     // waves along M
-  static constexpr int kWavesN = kDma ? 8 / kWavesM : 2;  // waves along N
-  static constexpr int kWaves = kWavesM * kWavesN;
+  static constexpr int kWavesN = kDma ? 8 / kWavesM / KS : 2;  // waves along N (K loop)
+  static constexpr int kWaves = kWavesM * kWavesN * KS;
   static constexpr int kThreads = 64 * kWaves;
-  static constexpr int kNT = BN / kWavesN / 32;          // 32-column subtiles per wave
+  static constexpr int kNT = BN / kWavesN / 32;          // 32-column subtiles per wave (K loop)
+  static constexpr int kNTE = kNT / KS;                  // ... in the epilogue
+  static constexpr int kWavesNE = kWavesN * KS;          // waves along N in the epilogue
+  // MFMA k-steps of one k-tile per wave (16-bit: 4 of 16; fp8: 2 of 64)
+  static constexpr int kKSteps = (IN_DT == DT_FP8 ? 2 : 4) / KS;
   static constexpr int kABlocksPerWave = TM / 8 / kWaves;  // 1 KiB load blocks of A
   static constexpr int kBBlocksPerWave = 16 / kWaves;      // ... and of B
   static constexpr int kAStageBytes = TM * kKTileBytes;
@@ -84,13 +99,26 @@ template <int IN_DT, int TM = 128> struct Cfg {
 // 4-float pad spreads the 32 rows one wave writes at a time over all banks).
 constexpr int kStagePitch = BN + 4;
 
-template <int IN_DT, int OUT_DT, int TM = 128> struct EpiLayout {
+// The exchange path's table of the row block's tile log-sum-exps, [slot][row]
+// with a row pitch of 129 floats (the 4 threads of a row read 4 slots from 4
+// different banks), for up to 64 column tiles.
+constexpr int kLsePitch = 129;
+
+template <int IN_DT, int OUT_DT, int TM = 128, int KS = 1, bool XCH = false> struct EpiLayout {
   static constexpr int STAGING = TM * kStagePitch * 4;
-  static constexpr int RING = Cfg<IN_DT, TM>::kRingBytes;
-  static constexpr int UNION = STAGING > RING ? STAGING : RING;
+  // exchange path: the log-sum-exp table follows the staged tile
+  static constexpr int LSE_OFF = (STAGING + 255) / 256 * 256;
+  static constexpr int LSE_END = XCH ? LSE_OFF + 64 * kLsePitch * 4 : STAGING;
+  static constexpr int RING = Cfg<IN_DT, TM, KS>::kRingBytes;
+  // k-split: each wave's half-block of partial sums (64 x 32 f32) passes
+  // through LDS once, in the ring after the last k-tile
+  static constexpr int KMERGE = KS == 2 ? 8 * 64 * 32 * 4 : 0;
+  static_assert(KMERGE <= RING, "k-split merge area");
+  static constexpr int UNION = LSE_END > RING ? LSE_END : RING;
   static constexpr int RED_OFF = (UNION + 255) / 256 * 256;
-  // wstat[kWavesN][TM] (float2), factor[kWavesN][TM] (float)
-  static constexpr int TOTAL = RED_OFF + 3 * Cfg<IN_DT, TM>::kWavesN * TM * 4;
+  // wstat[kWavesNE][TM] (float2), factor[kWavesNE][TM] (float), then the
+  // exchange path's tile log-sum-exps [TM] (float) and slot generations [64]
+  static constexpr int TOTAL = RED_OFF + 3 * Cfg<IN_DT, TM, KS>::kWavesNE * TM * 4 + TM * 4 + 64 * 4;
   static_assert(TOTAL <= 160 * 1024, "LDS");
 };
 
@@ -371,10 +399,10 @@ __device__ inline void mma_stage(const uint8_t* stage, int lane, int wm, int wn,
 }
 
 // All MFMA operands of one k-tile for one wave: A fragments [step][m-subtile],
-// B fragments [step][n-subtile].
-template <int NTN>
+// B fragments [step][n-subtile], for the wave's KSW k-steps.
+template <int NTN, int KSW>
 struct KTileFrags {
-  u32x4 a[4][2], b[4][NTN];
+  u32x4 a[KSW][2], b[KSW][NTN];
 };
 
 // Per-lane LDS offsets of a wave's fragment reads inside a stage.  Every read
@@ -382,32 +410,38 @@ struct KTileFrags {
 // 32 rows (4096 bytes: the A swizzle depends on row/2 mod 8 only), the
 // k-step and half (quad) of B add whole k-rows (its swizzle depends on k mod
 // 4, fp8: k/2 mod 4 only) -- so a step's reads need these few address
-// registers instead of one per read.  A: per k-step s the chunk 2s + lane/32
-// (16-bit) or, for fp8, entry 2s + hh for chunk 4s + 2(lane/32) + hh.  B: per
-// n-subtile, k-step 0, half / quad 0.
-template <bool F8, int NTN, int ASTAGE>
+// registers instead of one per read.  The wave runs k-steps s0 .. s0+KSW-1 of
+// each k-tile (s0 = 0 without a k-split).  A: per k-step s the chunk 2s +
+// lane/32 (16-bit) or, for fp8, entry 2s + hh for chunk 4s + 2(lane/32) + hh.
+// B: per n-subtile nt (first column nw + ((nt + rot) % NTN) * 32: a k-split
+// wave starts with its own epilogue slice), k-step s0, half / quad 0.
+template <bool F8, int NTN, int KSW, int ASTAGE>
 struct FragBase {
-  uint32_t a[4], b[NTN];
-  __device__ inline void init(int lane, int wm, int nw) {
+  static constexpr int NA = F8 ? 2 * KSW : KSW;
+  uint32_t a[NA], b[NTN];
+  __device__ inline void init(int lane, int wm, int nw, int rot, int s0) {
     const int r = frag_row(lane);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int c = F8 ? 4 * (i >> 1) + 2 * (lane >> 5) + (i & 1) : frag_chunk(lane, i);
+    for (int i = 0; i < NA; ++i) {
+      const int c = F8 ? 4 * (s0 + (i >> 1)) + 2 * (lane >> 5) + (i & 1) : frag_chunk(lane, s0 + i);
       a[i] = (uint32_t)a_lds_offset(wm * 64 + r, c);
     }
 #pragma unroll
-    for (int nt = 0; nt < NTN; ++nt)
-      b[nt] = (uint32_t)(ASTAGE + (F8 ? btr8_offset(btr8_k(0, 0, lane), btr8_n(nw + nt * 32, lane))
-                                      : btr_offset(btr_k(0, 0, lane), btr_n(nw + nt * 32, lane))));
+    for (int nt = 0; nt < NTN; ++nt) {
+      const int nb = nw + ((nt + rot) % NTN) * 32;
+      b[nt] = (uint32_t)(ASTAGE + (F8 ? btr8_offset(btr8_k(s0, 0, lane), btr8_n(nb, lane))
+                                      : btr_offset(btr_k(s0, 0, lane), btr_n(nb, lane))));
+    }
   }
 };
 
 // LDS read i of a k-tile's fragments (2 + 2*NTN reads per k-step s): the two
 // A fragments (ds_read_b128), then the halves of the NTN B fragments
 // (ds_read_b64_tr_b16).
-template <int NTN, int ASTAGE>
-__device__ inline void read_frag_piece(const uint8_t* stage, const FragBase<false, NTN, ASTAGE>& fb,
-                                       int i, KTileFrags<NTN>& f) {
+template <int NTN, int KSW, int ASTAGE>
+__device__ inline void read_frag_piece(const uint8_t* stage,
+                                       const FragBase<false, NTN, KSW, ASTAGE>& fb, int i,
+                                       KTileFrags<NTN, KSW>& f) {
   constexpr int RPS = 2 + 2 * NTN;
   const int s = i / RPS, u = i % RPS;
   if (u < 2) {
@@ -422,8 +456,8 @@ __device__ inline void read_frag_piece(const uint8_t* stage, const FragBase<fals
 
 // MFMA i of a k-tile (2*NTN per k-step): k-step i / (2*NTN), subtile
 // (mt, nt) = ((i / NTN) % 2, i % NTN).
-template <int IN_DT, int NTN>
-__device__ inline void mma_piece(const KTileFrags<NTN>& f, int i, f32x16 (&acc)[2][NTN]) {
+template <int IN_DT, int NTN, int KSW>
+__device__ inline void mma_piece(const KTileFrags<NTN, KSW>& f, int i, f32x16 (&acc)[2][NTN]) {
   const int s = i / (2 * NTN), mt = (i / NTN) & 1, nt = i % NTN;
   if constexpr (IN_DT == DT_F16) {
     acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
@@ -434,21 +468,22 @@ __device__ inline void mma_piece(const KTileFrags<NTN>& f, int i, f32x16 (&acc)[
   }
 }
 
-// fp8 (e4m3) operands of one k-tile (128 k = 2 MFMA k-steps of 64) for one
-// wave of 64 rows x 32*NTN columns: A [step][m-subtile][16-byte half],
-// B [step][n-subtile][8-byte transpose read].
-template <int NTN>
+// fp8 (e4m3) operands of one k-tile (128 k = 2 MFMA k-steps of 64; KSW of
+// them for this wave) for one wave of 64 rows x 32*NTN columns: A
+// [step][m-subtile][16-byte half], B [step][n-subtile][8-byte transpose read].
+template <int NTN, int KSW>
 struct KTileFrags8 {
-  u32x4 a[2][2][2];
-  u32x2 b[2][NTN][4];
+  u32x4 a[KSW][2][2];
+  u32x2 b[KSW][NTN][4];
 };
 
-// LDS read i (0 .. 2*(4+4*NTN)-1) of an fp8 k-tile's fragments: per k-step
+// LDS read i (0 .. KSW*(4+4*NTN)-1) of an fp8 k-tile's fragments: per k-step
 // s, reads 0-3 are the A halves (ds_read_b128: chunks 4s + 2(lane/32) + 0/1
 // of m-subtiles 0, 1), then four ds_read_b64_tr_b8 of B per n-subtile.
-template <int NTN, int ASTAGE>
-__device__ inline void read_frag_piece8(const uint8_t* stage, const FragBase<true, NTN, ASTAGE>& fb,
-                                        int i, KTileFrags8<NTN>& f) {
+template <int NTN, int KSW, int ASTAGE>
+__device__ inline void read_frag_piece8(const uint8_t* stage,
+                                        const FragBase<true, NTN, KSW, ASTAGE>& fb, int i,
+                                        KTileFrags8<NTN, KSW>& f) {
   constexpr int RPS = 4 + 4 * NTN;
   const int s = i / RPS, u = i % RPS;
   if (u < 4) {
@@ -460,11 +495,11 @@ __device__ inline void read_frag_piece8(const uint8_t* stage, const FragBase<tru
   }
 }
 
-// MFMA i (0 .. 4*NTN-1) of an fp8 k-tile: k-step i / (2*NTN), m-subtile
+// MFMA i (0 .. KSW*2*NTN-1) of an fp8 k-tile: k-step i / (2*NTN), m-subtile
 // (i / NTN) % 2, n-subtile i % NTN (v_mfma_f32_32x32x64_f8f6f4, both
 // operands e4m3, no block scales).
-template <int NTN>
-__device__ inline void mma_piece8(const KTileFrags8<NTN>& f, int i, f32x16 (&acc)[2][NTN]) {
+template <int NTN, int KSW>
+__device__ inline void mma_piece8(const KTileFrags8<NTN, KSW>& f, int i, f32x16 (&acc)[2][NTN]) {
   const int s = i / (2 * NTN), mt = (i / NTN) & 1, nt = i % NTN;
   const u32x4 a0 = f.a[s][mt][0], a1 = f.a[s][mt][1];
   const u32x2 b0 = f.b[s][nt][0], b1 = f.b[s][nt][1], b2 = f.b[s][nt][2], b3 = f.b[s][nt][3];
@@ -488,53 +523,58 @@ __device__ inline float2 load_stat(const float2* p) {
   return make_float2(__builtin_bit_cast(float, lo), __builtin_bit_cast(float, hi));
 }
 
-// Row-block barrier of the exchange path (called by one thread per tile once
-// the tile's statistics are stored).  Per row block the workspace holds an
-// arrival counter and a generation word, each in a cache line of its own
-// (kSyncWords apart per row block): polls of the generation word never
-// contend with the arrivals' atomic adds on the counter.  Each tile adds 1 to
-// the counter; the one that brings it to nT resets it to 0 and bumps the
-// generation; the others poll the generation until it differs from g0, the
-// value read at kernel start (it cannot move before this tile arrives, so
-// reading it early keeps it off the critical path).  The protocol keeps no
-// per-launch host state, so it survives graph replay, and the counter is
-// back at 0 after every launch, so a workspace may be reused for any shape.
+// ---- row exchange of the exchange path --------------------------------------
+// The tiles of a row block (all co-resident) exchange per-row log-sum-exps
+// through tagged entries instead of a barrier.  Tile (row block rbg, column
+// tile nt) owns slot rbg * nT + nt: 128 64-bit entries, one per tile row, at
+// ent + slot * 128.  An entry holds the row's log-sum-exp over the tile's
+// columns (f32, log2 domain) in its low word and a tag in its high word, and
+// is written with ONE 64-bit atomic store, so a reader sees either an old
+// entry or the whole new one.  The tag is the slot's generation + 1: every
+// slot has a generation word gen[slot]; the tiles of a row block read the
+// generation words of all its slots at kernel start, and the owner of a slot
+// increments its word at the end, after reading every other slot of its row
+// block.  An entry left by an earlier launch carries a tag <= the slot's
+// generation (a slot's entries are only ever written by the tile that owns
+// that slot index, whatever the problem shape), so a reader takes an entry
+// exactly when its tag equals generation + 1.  No counter, no ordering
+// between different words and no cache maintenance is needed, and there is
+// no per-launch host state (graph replays work).
 //
-// Memory ordering without cache maintenance: every word that crosses
-// workgroups here (statistics, counter, generation) is read and written only
-// with agent-scope atomics, which are coherent across the XCDs' L2s.  The
-// order that matters -- a tile's statistics are in place before its arrival
-// is counted, and are read only after the generation moved -- is enforced by
-// waiting for the statistics stores to complete (s_waitcnt) before the
-// counter RMW, and by issuing the statistics loads after the poll returned.
-// Agent-scope release/acquire fences would write back / invalidate the whole
-// L2 of the XCD, which costs far more than the exchange itself.
+// Why every reader has read gen[s] before the owner of s increments it: a
+// reader's generation loads have returned (the K loop ends with vmcnt(0))
+// before it stores its own entries; the owner of s increments gen[s] only
+// after loading those entries with this launch's tag.
 //
-// Returns once every tile of the row block has arrived, or after spin_ticks
-// of the 100 MHz clock (then err gets bit 0 and the tile goes on with what it
-// sees, so the kernel always drains).
-__device__ inline void rowblock_barrier(uint32_t* sync, uint32_t g0, int nT, uint32_t* err,
-                                        uint64_t spin_ticks) {
-  uint32_t* cnt = sync + kSyncCnt;
-  uint32_t* gen = sync + kSyncGen;
-  const uint32_t old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  if (old == (uint32_t)(nT - 1)) {
-    __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_fetch_add(gen, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return;
-  }
-  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-  uint64_t waited = 0;
-  while (__hip_atomic_load(gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == g0) {
-    __builtin_amdgcn_s_sleep(8);
-    waited = __builtin_amdgcn_s_memrealtime() - t0;
-    if (waited > spin_ticks) {
-      __hip_atomic_fetch_or(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_fetch_add(err + 2, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      break;
-    }
-  }
-  const uint32_t w32 = waited > 0xFFFFFFFFull ? 0xFFFFFFFFu : (uint32_t)waited;
+// Readers poll whole half-slots: one wave load takes 64 consecutive rows of
+// one slot (512 contiguous bytes), and a half-slot is done when every lane's
+// entry carries the expected tag; otherwise the wave sleeps briefly and
+// reloads only the half-slots not yet done.  Polling with wide, contiguous
+// loads keeps the traffic of the waits small, and there is no round trip
+// between learning that the data is there and loading it.
+//
+// Every wait is bounded by spin_ticks of the 100 MHz clock; a wait that runs
+// out sets bit 0 of err[0], counts in err[2], sets the caller's host-visible
+// mailbox word (if any), and the tile goes on with what it has, so the kernel
+// always drains.
+__device__ inline void store_entry(uint64_t* p, float lse, uint32_t tag) {
+  const uint64_t u = (uint64_t)__builtin_bit_cast(uint32_t, lse) | ((uint64_t)tag << 32);
+  __hip_atomic_store(p, u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline uint64_t load_entry(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline uint32_t entry_tag(uint64_t u) { return (uint32_t)(u >> 32); }
+__device__ inline float entry_lse(uint64_t u) { return __builtin_bit_cast(float, (uint32_t)u); }
+
+__device__ inline void report_timeout(uint32_t* err, uint32_t* mailbox) {
+  __hip_atomic_fetch_or(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_fetch_add(err + 2, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (mailbox) __hip_atomic_fetch_or(mailbox, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+__device__ inline void record_wait(uint32_t* err, uint64_t ticks) {
+  const uint32_t w32 = ticks > 0xFFFFFFFFull ? 0xFFFFFFFFu : (uint32_t)ticks;
   __hip_atomic_fetch_max(err + 1, w32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -557,18 +597,20 @@ constexpr int step_groups(int loads, int reads, int mfmas) {
 // workgroup count (gridDim.x would be read from the hidden kernel arguments
 // in memory).  Sizes and per-batch strides are 32-bit: the launcher keeps one
 // batch slice of A, B and out below 2 GiB.
-template <int IN_DT, int OUT_DT, int EPI, int PF, int TM>
-__global__ void __launch_bounds__((Cfg<IN_DT, TM>::kThreads), 1)
+template <int IN_DT, int OUT_DT, int EPI, int PF, int TM, int KS>
+__global__ void __launch_bounds__((Cfg<IN_DT, TM, KS>::kThreads), 1)
 chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32_t N32,
                   uint32_t K32, uint32_t lda32, uint32_t ldb32, uint32_t nT32, uint32_t nRB32,
                   uint32_t a_bs32, uint32_t b_bs32, uint32_t grid32, const ChainParams p) {
-  using C = Cfg<IN_DT, TM>;
-  using L = EpiLayout<IN_DT, OUT_DT, TM>;
+  using C = Cfg<IN_DT, TM, KS>;
+  using L = EpiLayout<IN_DT, OUT_DT, TM, KS, EPI == kEpiExchange>;
   static_assert(EPI != kEpiExchange || TM == 128, "the exchange path runs 128-row tiles");
   constexpr int BM = TM;  // tile rows
   constexpr int NT = C::kThreads;
-  constexpr int WN = C::kWavesN;
-  constexpr int NTN = C::kNT;
+  constexpr int WNK = C::kWavesN;  // waves along N in the K loop
+  constexpr int NTN = C::kNT;      // 32-column subtiles per wave in the K loop
+  constexpr int WN = C::kWavesNE;  // ... and in the epilogue
+  constexpr int NTE = C::kNTE;
   __shared__ __attribute__((aligned(16))) uint8_t smem[L::TOTAL];
   float2* wstat = reinterpret_cast<float2*>(smem + L::RED_OFF);  // [WN][BM] wave (max, sum)
   float* factor = reinterpret_cast<float*>(wstat + WN * BM);     // [WN][BM]
@@ -576,8 +618,11 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int wave = t >> 6;
-  const int wm = wave / WN, wn = wave % WN;
-  const int nw = wn * 32 * NTN;  // first column of the wave's block
+  // wave = (wm * WNK + wn_k) * KS + wk: k-split partners are adjacent waves
+  const int wk = wave % KS;
+  const int wm = wave / KS / WNK, wn_k = wave / KS % WNK;
+  const int wn = wn_k * KS + wk;  // the wave's column slice in the epilogue
+  const int nw = wn * 32 * NTE;   // first column of that slice
 
   uint32_t rbg, nt;  // row block across batches, column tile
   tile_of_block(blockIdx.x, grid32, grid32 / nT32, nT32, &rbg, &nt);
@@ -588,18 +633,19 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
 
   constexpr int SZ = dtype_bytes(IN_DT);
   const int nk = (int)(((uint64_t)K32 * SZ + kKTileBytes - 1) / kKTileBytes);
-  // The row block's generation word, as it is before this tile arrives (it
-  // cannot move until this tile has arrived).  Read by every lane,
-  // unconditionally, once the first k-tiles are requested: the load then
-  // stays in flight through the main loop.  (Under `if (t == 0)`, or ahead of
-  // the 32-bit multiply-adds of the load setup -- which the compiler emits as
+  // Exchange path: lane j of every wave reads the generation word of slot
+  // slot0 + j of the row block (lanes past nT re-read the last one), once the
+  // first k-tiles are requested: the load then stays in flight through the
+  // main loop.  Unconditional on purpose: under `if (t == 0)`, or ahead of the
+  // 32-bit multiply-adds of the load setup -- which the compiler emits as
   // 64-bit multiply-adds with an undefined high addend that may land on the
-  // load's destination register -- the compiler waits for it right there.)
-  uint32_t gen0 = 0;
+  // load's destination register -- the compiler waits for it right there.
+  const uint32_t slot0 = rbg * nT32;
+  uint32_t gen_lane = 0;
   auto load_gen0 = [&]() {
     if constexpr (EPI == kEpiExchange)
-      gen0 = __hip_atomic_load(p.sync + kSyncWords * rbg + kSyncGen, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
+      gen_lane = __hip_atomic_load(p.gen + slot0 + ((uint32_t)lane < nT32 ? (uint32_t)lane : nT32 - 1),
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   };
 
   f32x16 acc[2][NTN];
@@ -629,26 +675,28 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
     constexpr bool F8 = IN_DT == DT_FP8;
     using Plan = DmaPlan<IN_DT, C::kABlocksPerWave, C::kBBlocksPerWave, ASTAGE>;
     constexpr int LPT = Plan::LPT;                            // loads per wave per k-tile
-    constexpr int RPT = F8 ? 2 * (4 + 4 * NTN) : 4 * (2 + 2 * NTN);  // fragment reads
-    constexpr int MPT = F8 ? 4 * NTN : 4 * 2 * NTN;                  // MFMAs
+    constexpr int KSW = C::kKSteps;  // MFMA k-steps of a k-tile this wave runs
+    constexpr int RPT = F8 ? KSW * (4 + 4 * NTN) : KSW * (2 + 2 * NTN);  // fragment reads
+    constexpr int MPT = KSW * 2 * NTN;                                  // MFMAs
     // G groups per k-tile step: the fewest (>= LPT) that divide the reads
     // and the MFMAs evenly
     constexpr int G = step_groups(LPT, RPT, MPT);
     static_assert(G > 0, "k-tile step groups");
-    using Frags = std::conditional_t<F8, KTileFrags8<NTN>, KTileFrags<NTN>>;
-    FragBase<F8, NTN, ASTAGE> fb;
-    fb.init(lane, wm, nw);
+    using Frags = std::conditional_t<F8, KTileFrags8<NTN, KSW>, KTileFrags<NTN, KSW>>;
+    FragBase<F8, NTN, KSW, ASTAGE> fb;
+    // K-loop subtiles: the wave's epilogue slice first, then (k-split) the partner's
+    fb.init(lane, wm, wn_k * 32 * NTN, wk * NTE, wk * KSW);
     auto read_piece = [&](const uint8_t* st, int i, Frags& f) {
       if constexpr (F8)
-        read_frag_piece8<NTN, ASTAGE>(st, fb, i, f);
+        read_frag_piece8<NTN, KSW, ASTAGE>(st, fb, i, f);
       else
-        read_frag_piece<NTN, ASTAGE>(st, fb, i, f);
+        read_frag_piece<NTN, KSW, ASTAGE>(st, fb, i, f);
     };
     auto mma = [&](const Frags& f, int i) {
       if constexpr (F8)
-        mma_piece8<NTN>(f, i, acc);
+        mma_piece8<NTN, KSW>(f, i, acc);
       else
-        mma_piece<IN_DT>(f, i, acc);
+        mma_piece<IN_DT, NTN, KSW>(f, i, acc);
     };
     const int wave_u = __builtin_amdgcn_readfirstlane(wave);
     Plan d;
@@ -742,6 +790,31 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
     }
   }
 
+  // ---- k-split: merge the partners' partial sums --------------------------
+  // Every wave has passed its last LDS read (the K loop ends with a wait and a
+  // barrier), so the ring is free.  Each wave stores its partial sums of the
+  // partner's slice (subtiles NTE .. NTN-1), lane-major, 16 bytes per lane
+  // per store, and adds the partner's partial sums of its own slice.
+  if constexpr (KS == 2) {
+    static_assert(NTN == 2 && NTE == 1, "k-split pairs share a 64x64 block");
+    f32x4* xch = reinterpret_cast<f32x4*>(smem);  // [wave][mt][4 quads][64 lanes]
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        xch[(wave * 8 + mt * 4 + g) * 64 + lane] =
+            f32x4{acc[mt][1][4 * g], acc[mt][1][4 * g + 1], acc[mt][1][4 * g + 2], acc[mt][1][4 * g + 3]};
+    __syncthreads();
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const f32x4 v = xch[((wave ^ 1) * 8 + mt * 4 + g) * 64 + lane];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[mt][0][4 * g + e] += v[e];
+      }
+  }
+
   // ---- epilogue --------------------------------------------------------------
   // Lane owns output rows m_loc(mt) = wm*64 + mt*32 + lane%32 and, for each
   // n-subtile j, the 16 columns n_loc = nw + j*32 + acc_i(lane, v).  Each
@@ -755,7 +828,7 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-      for (int j = 0; j < NTN; ++j)
+      for (int j = 0; j < NTE; ++j)
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[mt][j][v] *= p.lin_scale;
   } else {
@@ -764,14 +837,14 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-        for (int j = 0; j < NTN; ++j)
+        for (int j = 0; j < NTE; ++j)
 #pragma unroll
           for (int v = 0; v < 16; ++v) acc[mt][j][v] *= p.c2;
     } else {
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-        for (int j = 0; j < NTN; ++j)
+        for (int j = 0; j < NTE; ++j)
 #pragma unroll
           for (int v = 0; v < 16; ++v) {
             const int n_loc = nw + j * 32 + acc_i(lane, v);
@@ -782,14 +855,14 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
     for (int mt = 0; mt < 2; ++mt) {
       float mx = -INFINITY;
 #pragma unroll
-      for (int j = 0; j < NTN; ++j)
+      for (int j = 0; j < NTE; ++j)
 #pragma unroll
         for (int v = 0; v < 16; ++v) mx = fmaxf(mx, acc[mt][j][v]);
       mx = wave_xor32_max(mx);
       const float base = mx == -INFINITY ? 0.0f : mx;  // every column of this wave past N
       float sm = 0.0f;
 #pragma unroll
-      for (int j = 0; j < NTN; ++j)
+      for (int j = 0; j < NTE; ++j)
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           const float e = __builtin_amdgcn_exp2f(acc[mt][j][v] - base);
@@ -817,23 +890,37 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
   // A row block of a single column tile (N <= 128) needs no exchange: the
   // tile's own statistics are the row's.
   const bool solo = EPI == kEpiExchange && nT32 == 1u;
+  // Exchange path: the row's log-sum-exp over this tile (log2 domain) per
+  // tile row, and the generation words of the row block's slots, in LDS.
+  float* tlse = factor + WN * BM;                             // [BM]
+  uint32_t* sgen = reinterpret_cast<uint32_t*>(tlse + BM);    // [64]
+  const uint32_t own_slot = slot0 + nt;
+  if constexpr (EPI == kEpiExchange)
+    if (t < 64 && (uint32_t)t < nT32) sgen[t] = gen_lane;
   if constexpr (EPI != kEpiLogits) {
-    __syncthreads();  // the wave statistics are in place
-    // Publish this tile's row statistics (partial[row block][row][column tile]).
-    if (t < BM && !solo) {
+    __syncthreads();  // the wave statistics (and slot generations) are in place
+    if (t < BM) {
       const float2 st = tile_stat(t);
-      store_stat(p.partial + ((int64_t)rbg * BM + t) * p.nT + nt, st.x, st.y);
+      if constexpr (EPI == kEpiExchange) {
+        // publish the row's log-sum-exp over this tile with this launch's tag
+        const float lse = st.x + __builtin_amdgcn_logf(st.y);
+        tlse[t] = lse;
+        if (!solo) store_entry(p.ent + (uint64_t)own_slot * BM + t, lse, sgen[nt] + 1u);
+      } else {
+        // split: per-tile (max, sumexp) for the rescale kernel
+        store_stat(p.partial + ((int64_t)rbg * BM + t) * p.nT + nt, st.x, st.y);
+      }
     }
   }
 
   // Stage the tile in LDS as f32 (the ring is free: every load has landed
-  // and every wave is past the last k-tile).  This overlaps the statistics
-  // stores and, on the exchange path, precedes the row-block wait.
+  // and every wave is past the last k-tile).  This overlaps the entry stores
+  // and, on the exchange path, precedes the wait for the other tiles.
   float* stg = reinterpret_cast<float*>(smem);
 #pragma unroll
   for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-    for (int j = 0; j < NTN; ++j)
+    for (int j = 0; j < NTE; ++j)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int m_loc = wm * 64 + mt * 32 + jr;
@@ -844,45 +931,80 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
       }
 
   if constexpr (EPI != kEpiLogits) {
-    if constexpr (EPI == kEpiExchange) {
-      if (!solo) {
-        if (t < BM) __builtin_amdgcn_s_waitcnt(0);  // statistics stores complete before this tile is counted
-        __syncthreads();
-        if (t == 0) rowblock_barrier(p.sync + kSyncWords * rbg, gen0, p.nT, p.err, p.spin_ticks);
-      }
-    }
     constexpr int P = NT / BM;  // threads per row (== WN)
     static_assert(P == WN, "one thread per (row, wave column slice)");
     const int r = t / P, h = t % P;
     if constexpr (EPI == kEpiExchange) {
-      __syncthreads();  // the row block's statistics are all in place
-      // The P threads of a row each merge a share of its nT (max, sum)
-      // pairs, loaded straight from the workspace in batches of 8
-      // independent loads, then combine with their partner lanes.
-      const int part = (p.nT + P - 1) / P;
-      const int q0 = solo ? 0 : (h * part < p.nT ? h * part : p.nT);
-      const int q1 = solo ? 0 : (q0 + part < p.nT ? q0 + part : p.nT);
-      const float2* st = p.partial + ((int64_t)rbg * BM + r) * p.nT;
-      float gm = -INFINITY, gs = 0.0f;
-      if (solo && h == 0) {  // the row's statistics from this tile's wave entries in LDS
-        const float2 ts = tile_stat(r);
-        gm = ts.x;
-        gs = ts.y;
-      }
-      for (int qb = q0; qb < q1; qb += 8) {
-        float2 v[8];
+      __syncthreads();  // tlse and sgen are in place
+      float gm = -INFINITY, gs = 0.0f;  // running max and sum of exp2(L - gm)
+      if (solo) {
+        if (h == 0) {  // the row's statistics from this tile's wave entries in LDS
+          const float2 ts = tile_stat(r);
+          gm = ts.x;
+          gs = ts.y;
+        }
+      } else {
+        // Wave w polls half-slots hs = w, w + NW, w + 2 NW, ... (slot hs / 2,
+        // rows (hs % 2) * 64 + lane), four at a time, and puts the
+        // log-sum-exps in the LDS table.  This tile's own slot comes from tlse.
+        constexpr int NW = NT / 64;  // waves
+        const int nT = (int)nT32;
+        float* lse_all = reinterpret_cast<float*>(smem + L::LSE_OFF);  // [slot][kLsePitch]
+        bool in_time = true;
+        uint64_t waited = 0;
+        for (int hb = wave; hb < 2 * nT; hb += 4 * NW) {
+          bool done[4];
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
-          v[u] = qb + u < q1 ? load_stat(st + qb + u) : make_float2(-INFINITY, 0.0f);
-        float cm = v[0].x;
+          for (int u = 0; u < 4; ++u) {
+            const int hs = hb + NW * u;
+            done[u] = !(hs < 2 * nT && (hs >> 1) != (int)nt);  // wave-uniform
+          }
+          const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+          for (;;) {
+            uint64_t e[4];
 #pragma unroll
-        for (int u = 1; u < 8; ++u) cm = fmaxf(cm, v[u].x);
-        const float nm = fmaxf(gm, cm);
-        float cs = gs * __builtin_amdgcn_exp2f(gm - nm);
+            for (int u = 0; u < 4; ++u) {
+              const int hs = hb + NW * u;
+              if (!done[u])
+                e[u] = load_entry(p.ent + (uint64_t)(slot0 + (hs >> 1)) * BM + (hs & 1) * 64 + lane);
+            }
+            bool all = true;
 #pragma unroll
-        for (int u = 0; u < 8; ++u) cs += v[u].y * __builtin_amdgcn_exp2f(v[u].x - nm);
-        gm = nm;
-        gs = cs;
+            for (int u = 0; u < 4; ++u) {
+              const int hs = hb + NW * u, q = hs >> 1;
+              if (!done[u]) {
+                if (__all(entry_tag(e[u]) == sgen[q] + 1u) || !in_time) {
+                  done[u] = true;
+                  lse_all[q * kLsePitch + (hs & 1) * 64 + lane] = entry_lse(e[u]);
+                } else {
+                  all = false;
+                }
+              }
+            }
+            if (all) break;
+            __builtin_amdgcn_s_sleep(1);
+            const uint64_t w = __builtin_amdgcn_s_memrealtime() - t0;
+            waited = w > waited ? w : waited;
+            if (w > p.spin_ticks) in_time = false;  // one more pass takes what is there
+          }
+        }
+        if (lane == 0 && waited > 0) {
+          record_wait(p.err, waited);
+          if (!in_time) report_timeout(p.err, p.mailbox);
+        }
+        __syncthreads();  // the table is complete
+        // The P threads of a row each merge a share of its nT tile
+        // log-sum-exps, then combine with their partner lanes.
+        const int part = (nT + P - 1) / P;
+        const int q0 = h * part < nT ? h * part : nT;
+        const int q1 = q0 + part < nT ? q0 + part : nT;
+        for (int q = q0; q < q1; ++q) {
+          const float Lq = q == (int)nt ? tlse[r] : lse_all[q * kLsePitch + r];
+          const float nm = fmaxf(gm, Lq);
+          gs = (gm == -INFINITY ? 0.0f : gs * __builtin_amdgcn_exp2f(gm - nm)) +
+               __builtin_amdgcn_exp2f(Lq - nm);
+          gm = nm;
+        }
       }
       // gm == -inf only for an empty share; its sum is 0
 #pragma unroll
@@ -893,7 +1015,8 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
              (om == -INFINITY ? 0.0f : os * __builtin_amdgcn_exp2f(om - M));
         gm = M;
       }
-      // thread (r, h) owns the factor of row r, column slice of wave h
+      // thread (r, h) owns the factor of row r, column slice of wave h:
+      // exp2(m_w - max) / sum, with (max, sum) over the whole row
       const float mw = wstat[h * BM + r].x;
       factor[h * BM + r] = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - gm) / gs;
     } else {
@@ -903,6 +1026,11 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
     }
   }
   __syncthreads();
+  // Every thread has its entries of the other slots: the next launch's
+  // entries of this tile's slot may carry the next tag.
+  if constexpr (EPI == kEpiExchange)
+    if (t == 0 && !solo)
+      __hip_atomic_store(p.gen + own_slot, sgen[nt] + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
   // ---- scale, convert and store: 16 output bytes per thread per step -------
   // The exchange path writes final outputs that this launch never reads
@@ -925,7 +1053,7 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
     const int64_t m = row0 + row;
     const int64_t n = n0 + ch * EPC;
     if (m < p.M && n < p.N) {
-      const float f = EPI == kEpiLogits ? 1.0f : factor[(ch * EPC / (32 * NTN)) * BM + row];
+      const float f = EPI == kEpiLogits ? 1.0f : factor[(ch * EPC / (32 * NTE)) * BM + row];
       const float* src = stg + row * kStagePitch + ch * EPC;
       const f32x4 x0 = *reinterpret_cast<const f32x4*>(src) * f;
       if constexpr (OSZ == 4) {
@@ -1041,17 +1169,17 @@ __global__ void zero_words_kernel(uint32_t* __restrict__ p, int64_t n) {
 // -------------------------------------------------------------------------
 constexpr int kPF = 3;
 
-template <int IN_DT, int OUT_DT, int EPI, int TM>
+template <int IN_DT, int OUT_DT, int EPI, int TM, int KS>
 static const void* tile_kernel_ptr() {
-  return reinterpret_cast<const void*>(&chain_tile_kernel<IN_DT, OUT_DT, EPI, kPF, TM>);
+  return reinterpret_cast<const void*>(&chain_tile_kernel<IN_DT, OUT_DT, EPI, kPF, TM, KS>);
 }
 
-template <int IN_DT, int EPI, int TM>
+template <int IN_DT, int EPI, int TM, int KS>
 static const void* by_out(int out_dt) {
   switch (out_dt) {
-    case DT_F32: return tile_kernel_ptr<IN_DT, DT_F32, EPI, TM>();
-    case DT_F16: return tile_kernel_ptr<IN_DT, DT_F16, EPI, TM>();
-    case DT_BF16: return tile_kernel_ptr<IN_DT, DT_BF16, EPI, TM>();
+    case DT_F32: return tile_kernel_ptr<IN_DT, DT_F32, EPI, TM, KS>();
+    case DT_F16: return tile_kernel_ptr<IN_DT, DT_F16, EPI, TM, KS>();
+    case DT_BF16: return tile_kernel_ptr<IN_DT, DT_BF16, EPI, TM, KS>();
   }
   return nullptr;
 }
@@ -1059,10 +1187,21 @@ static const void* by_out(int out_dt) {
 template <int EPI>
 static const void* by_in(int in_dt, int out_dt) {
   switch (in_dt) {
-    case DT_F32: return by_out<DT_F32, EPI, 128>(out_dt);
-    case DT_F16: return by_out<DT_F16, EPI, 128>(out_dt);
-    case DT_BF16: return by_out<DT_BF16, EPI, 128>(out_dt);
-    case DT_FP8: return by_out<DT_FP8, EPI, 128>(out_dt);
+    case DT_F32: return by_out<DT_F32, EPI, 128, 1>(out_dt);
+    case DT_F16: return by_out<DT_F16, EPI, 128, 1>(out_dt);
+    case DT_BF16: return by_out<DT_BF16, EPI, 128, 1>(out_dt);
+    case DT_FP8: return by_out<DT_FP8, EPI, 128, 1>(out_dt);
+  }
+  return nullptr;
+}
+
+// 128-row tiles with the k-split wave layout (16-bit and fp8 inputs).
+template <int EPI>
+static const void* ksplit_by_in(int in_dt, int out_dt) {
+  switch (in_dt) {
+    case DT_F16: return by_out<DT_F16, EPI, 128, 2>(out_dt);
+    case DT_BF16: return by_out<DT_BF16, EPI, 128, 2>(out_dt);
+    case DT_FP8: return by_out<DT_FP8, EPI, 128, 2>(out_dt);
   }
   return nullptr;
 }
@@ -1070,16 +1209,22 @@ static const void* by_in(int in_dt, int out_dt) {
 // 256-row tiles: the split path with 16-bit or fp8 inputs.
 static const void* split256_by_in(int in_dt, int out_dt) {
   switch (in_dt) {
-    case DT_F16: return by_out<DT_F16, kEpiSplit, 256>(out_dt);
-    case DT_BF16: return by_out<DT_BF16, kEpiSplit, 256>(out_dt);
-    case DT_FP8: return by_out<DT_FP8, kEpiSplit, 256>(out_dt);
+    case DT_F16: return by_out<DT_F16, kEpiSplit, 256, 1>(out_dt);
+    case DT_BF16: return by_out<DT_BF16, kEpiSplit, 256, 1>(out_dt);
+    case DT_FP8: return by_out<DT_FP8, kEpiSplit, 256, 1>(out_dt);
   }
   return nullptr;
 }
 
-const void* chain_kernel_symbol(int in_dt, int out_dt, int epi, int tile_rows) {
-  if (tile_rows == 256) return epi == kEpiSplit ? split256_by_in(in_dt, out_dt) : nullptr;
+const void* chain_kernel_symbol(int in_dt, int out_dt, int epi, int tile_rows, int ks) {
+  if (tile_rows == 256) return epi == kEpiSplit && ks == 1 ? split256_by_in(in_dt, out_dt) : nullptr;
   if (tile_rows != 128) return nullptr;
+  if (ks == 2) {
+    if (epi == kEpiExchange) return ksplit_by_in<kEpiExchange>(in_dt, out_dt);
+    if (epi == kEpiSplit) return ksplit_by_in<kEpiSplit>(in_dt, out_dt);
+    return nullptr;
+  }
+  if (ks != 1) return nullptr;
   if (epi == kEpiExchange) return by_in<kEpiExchange>(in_dt, out_dt);
   if (epi == kEpiSplit) return by_in<kEpiSplit>(in_dt, out_dt);
   if (epi == kEpiLogits) return by_in<kEpiLogits>(in_dt, out_dt);
@@ -1097,12 +1242,12 @@ const void* rescale_kernel_symbol(int out_dt) {
 
 const void* zero_kernel_symbol() { return reinterpret_cast<const void*>(&zero_words_kernel); }
 
-template <int IN_DT>
+template <int IN_DT, int KS>
 static int lds_bytes_for(int out_dt) {
   switch (out_dt) {
-    case DT_F32: return EpiLayout<IN_DT, DT_F32>::TOTAL;
-    case DT_F16: return EpiLayout<IN_DT, DT_F16>::TOTAL;
-    case DT_BF16: return EpiLayout<IN_DT, DT_BF16>::TOTAL;
+    case DT_F32: return EpiLayout<IN_DT, DT_F32, 128, KS, true>::TOTAL;
+    case DT_F16: return EpiLayout<IN_DT, DT_F16, 128, KS, true>::TOTAL;
+    case DT_BF16: return EpiLayout<IN_DT, DT_BF16, 128, KS, true>::TOTAL;
   }
   return 0;
 }
@@ -1117,12 +1262,20 @@ int chain_kernel_threads(int in_dt) {
   return 0;
 }
 
-int chain_kernel_lds_bytes(int in_dt, int out_dt) {
+int chain_kernel_lds_bytes(int in_dt, int out_dt, int ks) {
+  if (ks == 2) {
+    switch (in_dt) {
+      case DT_F16: return lds_bytes_for<DT_F16, 2>(out_dt);
+      case DT_BF16: return lds_bytes_for<DT_BF16, 2>(out_dt);
+      case DT_FP8: return lds_bytes_for<DT_FP8, 2>(out_dt);
+    }
+    return 0;
+  }
   switch (in_dt) {
-    case DT_F32: return lds_bytes_for<DT_F32>(out_dt);
-    case DT_F16: return lds_bytes_for<DT_F16>(out_dt);
-    case DT_BF16: return lds_bytes_for<DT_BF16>(out_dt);
-    case DT_FP8: return lds_bytes_for<DT_FP8>(out_dt);
+    case DT_F32: return lds_bytes_for<DT_F32, 1>(out_dt);
+    case DT_F16: return lds_bytes_for<DT_F16, 1>(out_dt);
+    case DT_BF16: return lds_bytes_for<DT_BF16, 1>(out_dt);
+    case DT_FP8: return lds_bytes_for<DT_FP8, 1>(out_dt);
   }
   return 0;
 }

@@ -1,22 +1,23 @@
 // launch.hip -- host side of the launcher C-ABI (include/wtc/wtc_hip.h):
-// argument checks, the launch plan, the per-device default workspace, and
-// the kernel launches for the exchange, split and unfused paths.
+// argument checks, the launch plan, the per-stream default workspaces, the
+// host-visible timeout mailbox, the cross-stream ordering of exchange-path
+// calls, and the kernel launches for the exchange, split, row-block and
+// unfused paths.
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <vector>
 
 #include "tile_layout.h"
 #include "wtc/wtc_hip.h"
 #include "wtc_kernels.h"
 
-// Tile height of the split path: 256-row tiles (a quarter less L2 and a
-// third less LDS traffic per MFMA) for 16-bit and fp8 inputs when they add
-// no padding rows (an even number of 128-row blocks) and the problem still
-// gives every CU at least two of them; 128 otherwise.
 namespace wtc {
 // Waves of rescale_rows_kernel per row: enough for 16 waves per CU when rows
 // are few (wide rows), at most 8.
@@ -26,12 +27,20 @@ int rescale_waves_per_row(int64_t rows_total, int cu_count) {
   return wpr;
 }
 
+// Tile height of the split path: 256-row tiles (a quarter less L2 and a
+// third less LDS traffic per MFMA) for 16-bit and fp8 inputs when they add
+// no padding rows (an even number of 128-row blocks) and the problem still
+// gives every CU at least two of them; 128 otherwise.
 int split_tile_rows(int in_dt, int64_t batch, int64_t m, int64_t n, int cu_count) {
   if (in_dt == DT_F32) return 128;
   const int64_t rb128 = (m + 127) / 128;
   const int64_t tiles256 = batch * (rb128 / 2) * ((n + 127) / 128);
   return rb128 % 2 == 0 && tiles256 >= 2 * (int64_t)cu_count ? 256 : 128;
 }
+
+// Wave layout of the exchange path's 128-row tiles: k-split (ks = 2) for
+// 16-bit and fp8 inputs, 4 waves of 64x64 for f32.
+int exchange_ks(int in_dt) { return in_dt == DT_F32 ? 1 : 2; }
 }  // namespace wtc
 
 namespace {
@@ -39,14 +48,15 @@ namespace {
 using namespace wtc;
 
 constexpr int kTile = 128;            // BM = BN of chain_tile_kernel
-constexpr int kThreads = 256;  // the row kernels (rescale, unfused, zero fill)
 constexpr int kRescaleRowsPerWg = 4;  // rescale_rows_kernel
 constexpr int kRescaleMaxTiles = 512;
-constexpr int kExchangeMaxTiles = 64;        // row statistics staged in the 64 KiB LDS ring
-constexpr uint64_t kSpinTicks = 200000000ull;  // 2 s of the 100 MHz clock
+constexpr int kExchangeMaxColTiles = 64;  // one lane per column tile of a row block
+constexpr uint64_t kDefaultSpinTicks = 200000000ull;  // 2 s of the 100 MHz clock
 constexpr int kMaxDevices = 64;
+constexpr int64_t kMinDefaultWorkspace = 1 << 20;
 
 thread_local std::string g_last_error;
+std::atomic<uint64_t> g_spin_ticks{kDefaultSpinTicks};
 
 int fail(int code, const std::string& msg) {
   g_last_error = msg;
@@ -59,34 +69,34 @@ int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
 bool valid_in(int dt) { return dt == DT_F32 || dt == DT_F16 || dt == DT_BF16 || dt == DT_FP8; }
 bool valid_out(int dt) { return dt == DT_F32 || dt == DT_F16 || dt == DT_BF16; }
 
-// Workspace layout (bytes).  The counter region sits at a fixed place with a
-// fixed size, so a workspace reused across problem shapes never has one
-// call's statistics or logits land on another call's counters (the counters
-// are zeroed once and left at zero by every exchange launch).
-//   [0, 256)                       diagnostic words (flags, longest wait, timeouts)
-//   [256, 256 + kSyncRegion)       row-block counter / generation lines
-//   [.., +partial)                 per-tile row statistics, float2 [rows_pad][nT]
-//   [.., +logits)                  unfused path only: f32 logits, row max, row sum
-constexpr int64_t kMaxSyncRowBlocks = 512;
-constexpr int64_t kSyncRegion = kMaxSyncRowBlocks * kSyncWords * 4;
+// Workspace layout (bytes).  The slot generation words sit at a fixed place
+// with a fixed size, and a slot's exchange entries at a fixed place
+// (slot * 1 KiB into the statistics region), so a workspace reused across
+// problem shapes never mistakes another call's data for its own.
+//   [0, 256)                 diagnostic words (flags, longest wait, timeouts)
+//   [256, 256 + 4 KiB)       exchange slot generation words
+//   [.., +stats)             split: float2 [batch][rows padded to 256][nT];
+//                            exchange: uint64 [tiles][128] tagged entries
+//   [.., +logits)            unfused path only: f32 logits, row max, row sum
+constexpr int64_t kGenOff = 256;
+constexpr int64_t kGenBytes = (int64_t)kMaxExchangeTiles * 4;
 
 struct WsLayout {
-  int64_t sync_off, sync_bytes;
-  int64_t partial_off, partial_bytes;
+  int64_t gen_off, stats_off, stats_bytes;
   int64_t logits_off, max_off, sum_off;
   int64_t total;
 };
 
 WsLayout ws_layout(int64_t batch, int64_t m, int64_t n, int path) {
   WsLayout w{};
-  const int64_t nRB = ceil_div(m, kTile), nT = ceil_div(n, kTile);
-  const int64_t rbs = batch * nRB;
-  w.sync_off = 256;
-  w.sync_bytes = kSyncRegion;
-  w.partial_off = w.sync_off + w.sync_bytes;
-  // statistics rows padded to 256 per batch (either tile height of the split path)
-  w.partial_bytes = align256(batch * ceil_div(m, 256) * 256 * nT * 8);
-  w.total = w.partial_off + w.partial_bytes;
+  const int64_t nT = ceil_div(n, kTile);
+  w.gen_off = kGenOff;
+  w.stats_off = align256(kGenOff + kGenBytes);
+  // split statistics rows padded to 256 per batch (either tile height)
+  const int64_t split_bytes = batch * ceil_div(m, 256) * 256 * nT * 8;
+  const int64_t exch_bytes = batch * ceil_div(m, kTile) * nT * kTile * 8;
+  w.stats_bytes = align256(split_bytes > exch_bytes ? split_bytes : exch_bytes);
+  w.total = w.stats_off + w.stats_bytes;
   if (path == WTC_PATH_UNFUSED) {
     w.logits_off = w.total;
     w.max_off = w.logits_off + align256(batch * m * n * 4);
@@ -125,7 +135,7 @@ int plan_impl(int64_t batch, int64_t m, int64_t n, int64_t k, int in_dt, int out
   int p = path;
   const int64_t nT = ceil_div(n, kTile);
   const int64_t rbs = batch * ceil_div(m, kTile);
-  const bool fits = tiles <= capacity && nT <= kExchangeMaxTiles && rbs <= kMaxSyncRowBlocks;
+  const bool fits = tiles <= capacity && nT <= kExchangeMaxColTiles && tiles <= kMaxExchangeTiles;
   const bool rows_ok = (in_dt == DT_F16 || in_dt == DT_BF16) && k <= rows_kernel_max_k();
   if (p == WTC_PATH_AUTO) {
     if (rows_ok && (!fits || rbs >= (int64_t)cu_count))
@@ -140,8 +150,9 @@ int plan_impl(int64_t batch, int64_t m, int64_t n, int64_t k, int in_dt, int out
     return fail(WTC_ERR_UNSUPPORTED,
                 "exchange path needs every tile co-resident: " + std::to_string(tiles) +
                     " tiles > " + std::to_string(capacity) + " resident workgroups");
-  if (p == WTC_PATH_EXCHANGE && (nT > kExchangeMaxTiles || rbs > kMaxSyncRowBlocks))
-    return fail(WTC_ERR_UNSUPPORTED, "exchange path supports n <= 8192 and <= 512 row blocks");
+  if (p == WTC_PATH_EXCHANGE && (nT > kExchangeMaxColTiles || tiles > kMaxExchangeTiles))
+    return fail(WTC_ERR_UNSUPPORTED, "exchange path supports n <= 8192 and <= " +
+                                         std::to_string(kMaxExchangeTiles) + " tiles");
   if (p == WTC_PATH_SPLIT && ceil_div(n, kTile) > kRescaleMaxTiles)
     return fail(WTC_ERR_UNSUPPORTED, "split path supports n <= 65536");
   if (tiles > 0x7FFFFFFFll) return fail(WTC_ERR_UNSUPPORTED, "too many tiles for one grid");
@@ -158,12 +169,30 @@ int plan_impl(int64_t batch, int64_t m, int64_t n, int64_t k, int in_dt, int out
   return WTC_OK;
 }
 
+// A default workspace of one stream.  Grow-only: a superseded buffer is kept
+// (in `retired`) until the process ends, because a graph captured earlier may
+// still hold its address.
+struct StreamWorkspace {
+  hipStream_t stream;
+  void* ptr;
+  size_t bytes;
+};
+
 struct DeviceState {
   bool init = false;
   int cu_count = 0;
   int occ[4][3] = {};  // exchange-kernel workgroups per CU, [in_dt][out_dt]
-  void* ws = nullptr;
-  size_t ws_bytes = 0;
+  std::vector<StreamWorkspace> ws;
+  std::vector<void*> retired;
+  // Host-visible word the exchange kernels set when a wait times out
+  // (pinned, mapped host memory): the next call on the device reports it.
+  volatile uint32_t* mailbox_host = nullptr;
+  uint32_t* mailbox_dev = nullptr;
+  // Cross-stream ordering of exchange-path calls: an event recorded after
+  // every exchange launch, and the stream it was recorded on.
+  hipEvent_t exch_event = nullptr;
+  hipStream_t exch_stream = nullptr;
+  bool exch_used = false;
 };
 
 std::mutex g_mu;
@@ -179,7 +208,7 @@ DeviceState g_dev[kMaxDevices];
 // Dynamic LDS added to the exchange kernel so that no CU holds two of its
 // workgroups (spreads a grid of <= CU-count tiles over all CUs).
 int exchange_lds_pad(int in_dt, int out_dt) {
-  const int stat = chain_kernel_lds_bytes(in_dt, out_dt);
+  const int stat = chain_kernel_lds_bytes(in_dt, out_dt, exchange_ks(in_dt));
   const int want = 80 * 1024 + 1024;
   return stat >= want ? 0 : want - stat;
 }
@@ -193,13 +222,22 @@ int device_state(int dev, DeviceState** out) {
     s.cu_count = prop.multiProcessorCount;
     for (int i = 0; i < 4; ++i)
       for (int o = 0; o < 3; ++o) {
-        const void* fn = chain_kernel_symbol(i, o, kEpiExchange);
+        const void* fn = chain_kernel_symbol(i, o, kEpiExchange, 128, exchange_ks(i));
         const int pad = exchange_lds_pad(i, o);
         HIP_TRY(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, pad));
         int nb = 0;
         HIP_TRY(hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, fn, chain_kernel_threads(i), pad));
         s.occ[i][o] = nb;
       }
+    void* mb = nullptr;
+    HIP_TRY(hipHostMalloc(&mb, 64, hipHostMallocMapped | hipHostMallocCoherent));
+    std::memset(mb, 0, 64);
+    void* mbd = nullptr;
+    HIP_TRY(hipHostGetDevicePointer(&mbd, mb, 0));
+    s.mailbox_host = static_cast<volatile uint32_t*>(mb);
+    s.mailbox_dev = static_cast<uint32_t*>(mbd);
+    // ordering between streams of one device only: no system-scope fence
+    HIP_TRY(hipEventCreateWithFlags(&s.exch_event, hipEventDisableTiming | hipEventDisableSystemFence));
     s.init = true;
   }
   *out = &s;
@@ -218,18 +256,44 @@ int zero_fill(void* p, int64_t bytes, hipStream_t stream) {
   return WTC_OK;
 }
 
+bool stream_capturing(hipStream_t stream) {
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &st) != hipSuccess) return false;
+  return st != hipStreamCaptureStatusNone;
+}
+
+// The default workspace of `stream` with at least `need` bytes, zeroed on
+// that stream when first allocated.  No allocation while the stream is being
+// captured into a graph.
 int default_workspace(DeviceState* s, int64_t need, void** ws, hipStream_t stream) {
-  if ((int64_t)s->ws_bytes < need) {
-    if (s->ws) HIP_TRY(hipFree(s->ws));
-    s->ws = nullptr;
-    s->ws_bytes = 0;
-    const int64_t bytes = need < (1 << 20) ? (1 << 20) : need;
-    HIP_TRY(hipMalloc(&s->ws, (size_t)bytes));
-    s->ws_bytes = (size_t)bytes;
-    int rc = zero_fill(s->ws, bytes, stream);
-    if (rc) return rc;
+  StreamWorkspace* cur = nullptr;
+  for (StreamWorkspace& w : s->ws)
+    if (w.stream == stream) cur = &w;
+  if (cur && (int64_t)cur->bytes >= need) {
+    *ws = cur->ptr;
+    return WTC_OK;
   }
-  *ws = s->ws;
+  if (stream_capturing(stream))
+    return fail(WTC_ERR_ARG,
+                "the stream is being captured and its default workspace would have to be "
+                "allocated: pass a workspace, or make one call of this shape on this stream "
+                "before capturing");
+  const int64_t bytes = need < kMinDefaultWorkspace ? kMinDefaultWorkspace : need;
+  void* p = nullptr;
+  HIP_TRY(hipMalloc(&p, (size_t)bytes));
+  int rc = zero_fill(p, bytes, stream);
+  if (rc) {
+    (void)hipFree(p);
+    return rc;
+  }
+  if (cur) {
+    s->retired.push_back(cur->ptr);
+    cur->ptr = p;
+    cur->bytes = (size_t)bytes;
+  } else {
+    s->ws.push_back(StreamWorkspace{stream, p, (size_t)bytes});
+  }
+  *ws = p;
   return WTC_OK;
 }
 
@@ -244,8 +308,11 @@ int launch_chain(const void* kern, int threads, int64_t grid, int lds_dyn,
 // chain_tile_kernel: the scalars a tile needs before its first load lead the
 // argument list (preloaded into SGPRs), then the parameter block.  check_args
 // keeps every batch slice below 2 GiB, so the 32-bit sizes and strides hold.
+// `done`, if given, is an event that completes with the kernel: attached to
+// the launch itself (hipExtLaunchKernel), it costs nothing, where a separate
+// hipEventRecord after the launch adds a gap of 1-3 us between kernels.
 int launch_tile(const void* kern, int threads, int64_t grid, int lds_dyn,
-                const ChainParams& prm, hipStream_t stream) {
+                const ChainParams& prm, hipStream_t stream, hipEvent_t done = nullptr) {
   ChainParams p = prm;
   const uint8_t* a = p.a;
   const uint8_t* b = p.b;
@@ -255,7 +322,40 @@ int launch_tile(const void* kern, int threads, int64_t grid, int lds_dyn,
   uint32_t a_bs = (uint32_t)p.a_bstride, b_bs = (uint32_t)p.b_bstride;
   uint32_t g = (uint32_t)grid;
   void* args[] = {&a, &b, &M, &N, &K, &lda, &ldb, &nT, &nRB, &a_bs, &b_bs, &g, &p};
-  HIP_TRY(hipLaunchKernel(kern, dim3((unsigned)grid), dim3(threads), args, (size_t)lds_dyn, stream));
+  if (done)
+    HIP_TRY(hipExtLaunchKernel(kern, dim3((unsigned)grid), dim3(threads), args, (size_t)lds_dyn,
+                               stream, nullptr, done, 0));
+  else
+    HIP_TRY(hipLaunchKernel(kern, dim3((unsigned)grid), dim3(threads), args, (size_t)lds_dyn, stream));
+  return WTC_OK;
+}
+
+// A timed-out exchange wait of an earlier call on this device, reported once.
+int take_mailbox(DeviceState* ds) {
+  if (ds->mailbox_host && *ds->mailbox_host != 0u &&
+      __atomic_exchange_n(const_cast<uint32_t*>(ds->mailbox_host), 0u, __ATOMIC_SEQ_CST) != 0u) {
+    return fail(WTC_ERR_TIMEOUT,
+                "an exchange-path wait of an earlier call on this device timed out (its tiles "
+                "were not all resident at once); that call's output is wrong");
+  }
+  return WTC_OK;
+}
+
+// Exchange-path calls on one device must not overlap (each needs all of its
+// tiles resident).  Calls from this process on different streams are put in
+// order: every exchange launch completes the device's exchange event, and a
+// call on another stream first waits for it.  Not done for streams being
+// captured into a graph (an event completed outside a capture cannot order
+// it, nor can the capture complete it).
+int launch_exchange(DeviceState* ds, const void* kern, int threads, int64_t grid, int lds_dyn,
+                    const ChainParams& p, hipStream_t stream) {
+  if (stream_capturing(stream)) return launch_tile(kern, threads, grid, lds_dyn, p, stream);
+  if (ds->exch_used && stream != ds->exch_stream)
+    HIP_TRY(hipStreamWaitEvent(stream, ds->exch_event, 0));
+  const int rc = launch_tile(kern, threads, grid, lds_dyn, p, stream, ds->exch_event);
+  if (rc) return rc;
+  ds->exch_used = true;
+  ds->exch_stream = stream;
   return WTC_OK;
 }
 
@@ -265,7 +365,7 @@ extern "C" {
 
 const char* wtc_last_error(void) { return g_last_error.c_str(); }
 
-const char* wtc_version(void) { return "wtc-mi355x 0.1.0 (gfx950)"; }
+const char* wtc_version(void) { return "wtc-mi355x 0.2.0 (gfx950)"; }
 
 int wtc_plan(int64_t batch, int64_t m, int64_t n, int64_t k, int in_dtype, int out_dtype,
              int path, int cu_count, int wg_per_cu, int64_t* grid, int* chosen_path,
@@ -288,25 +388,49 @@ int wtc_workspace_init(void* workspace, size_t workspace_bytes, void* stream) {
   return zero_fill(workspace, (int64_t)workspace_bytes, static_cast<hipStream_t>(stream));
 }
 
+int wtc_set_exchange_wait_limit(uint64_t ticks) {
+  g_last_error.clear();
+  g_spin_ticks.store(ticks ? ticks : kDefaultSpinTicks);
+  return WTC_OK;
+}
+
+int wtc_check_status(void* stream) {
+  g_last_error.clear();
+  int dev = 0;
+  HIP_TRY(hipGetDevice(&dev));
+  HIP_TRY(hipStreamSynchronize(static_cast<hipStream_t>(stream)));
+  std::lock_guard<std::mutex> lk(g_mu);
+  DeviceState* ds = nullptr;
+  int rc = device_state(dev, &ds);
+  if (rc) return rc;
+  return take_mailbox(ds);
+}
+
 int wtc_read_error_flags(void* workspace, uint32_t* flags, int clear) {
   g_last_error.clear();
   if (!flags) return fail(WTC_ERR_ARG, "flags is NULL");
-  void* ws = workspace;
-  if (!ws) {
+  flags[0] = flags[1] = flags[2] = 0;
+  std::vector<void*> bufs;
+  if (workspace) {
+    bufs.push_back(workspace);
+  } else {
     int dev = 0;
     HIP_TRY(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices) return fail(WTC_ERR_HIP, "device index out of range");
     std::lock_guard<std::mutex> lk(g_mu);
-    if (dev < 0 || dev >= kMaxDevices || !g_dev[dev].ws) {
-      flags[0] = flags[1] = flags[2] = 0;
-      return WTC_OK;
-    }
-    ws = g_dev[dev].ws;
+    for (const StreamWorkspace& w : g_dev[dev].ws) bufs.push_back(w.ptr);
   }
   HIP_TRY(hipDeviceSynchronize());
-  HIP_TRY(hipMemcpy(flags, ws, 3 * sizeof(uint32_t), hipMemcpyDeviceToHost));
-  if (clear) {
-    const uint32_t zero[3] = {0, 0, 0};
-    HIP_TRY(hipMemcpy(ws, zero, sizeof zero, hipMemcpyHostToDevice));
+  for (void* b : bufs) {
+    uint32_t w[3];
+    HIP_TRY(hipMemcpy(w, b, sizeof w, hipMemcpyDeviceToHost));
+    flags[0] |= w[0];
+    flags[1] = w[1] > flags[1] ? w[1] : flags[1];
+    flags[2] += w[2];
+    if (clear) {
+      const uint32_t zero[3] = {0, 0, 0};
+      HIP_TRY(hipMemcpy(b, zero, sizeof zero, hipMemcpyHostToDevice));
+    }
   }
   return WTC_OK;
 }
@@ -332,6 +456,8 @@ int wtc_matmul_softmax(const void* a, const void* b, void* out, int64_t batch, i
   std::lock_guard<std::mutex> lk(g_mu);
   DeviceState* ds = nullptr;
   rc = device_state(dev, &ds);
+  if (rc) return rc;
+  rc = take_mailbox(ds);
   if (rc) return rc;
 
   int64_t grid = 0, need = 0;
@@ -375,23 +501,25 @@ int wtc_matmul_softmax(const void* a, const void* b, void* out, int64_t batch, i
       chosen == WTC_PATH_SPLIT ? split_tile_rows(in_dtype, batch, m, n, ds->cu_count) : kTile;
   p.nRB = (int)ceil_div(m, tile_rows);
   p.nT = (int)ceil_div(n, kTile);
-  p.partial = reinterpret_cast<float2*>(wsb + L.partial_off);
-  p.sync = reinterpret_cast<uint32_t*>(wsb + L.sync_off);
+  p.partial = reinterpret_cast<float2*>(wsb + L.stats_off);
+  p.ent = reinterpret_cast<uint64_t*>(wsb + L.stats_off);
+  p.gen = reinterpret_cast<uint32_t*>(wsb + L.gen_off);
   p.err = reinterpret_cast<uint32_t*>(wsb);
-  p.spin_ticks = kSpinTicks;
+  p.mailbox = ds->mailbox_dev;
+  p.spin_ticks = g_spin_ticks.load();
 
   if (chosen == WTC_PATH_ROWS) {
     return launch_chain(rows_kernel_symbol(in_dtype, out_dtype), rows_kernel_threads(), grid, 0,
                         p, stream);
   }
-  if (chosen == WTC_PATH_EXCHANGE) {
-    return launch_tile(chain_kernel_symbol(in_dtype, out_dtype, kEpiExchange),
-                        chain_kernel_threads(in_dtype), grid,
-                        exchange_lds_pad(in_dtype, out_dtype), p, stream);
-  }
+  if (chosen == WTC_PATH_EXCHANGE)
+    return launch_exchange(ds,
+                           chain_kernel_symbol(in_dtype, out_dtype, kEpiExchange, 128, exchange_ks(in_dtype)),
+                           chain_kernel_threads(in_dtype), grid, exchange_lds_pad(in_dtype, out_dtype), p,
+                           stream);
   if (chosen == WTC_PATH_SPLIT) {
     rc = launch_tile(chain_kernel_symbol(in_dtype, out_dtype, kEpiSplit, tile_rows),
-                      chain_kernel_threads(in_dtype), grid, 0, p, stream);
+                     chain_kernel_threads(in_dtype), grid, 0, p, stream);
     if (rc) return rc;
     uint8_t* o = p.out;
     const float2* part = p.partial;

@@ -10,12 +10,10 @@ namespace wtc {
 
 enum : int { kEpiExchange = 0, kEpiSplit = 1, kEpiLogits = 2 };
 
-// 32-bit words of workspace per row block for the exchange: the arrival
-// counter at word kSyncCnt and the generation word at kSyncGen, each in a
-// 128-byte line of its own.
-constexpr int kSyncWords = 64;
-constexpr int kSyncCnt = 0;
-constexpr int kSyncGen = 32;
+// The exchange path keeps one generation word per tile slot (slot = row
+// block * column tiles + column tile) and 128 tagged 64-bit entries per slot;
+// a launch uses at most this many slots.
+constexpr int kMaxExchangeTiles = 1024;
 
 struct ChainParams {
   const uint8_t* a;
@@ -28,20 +26,24 @@ struct ChainParams {
   float lin_scale;  // scale for kEpiLogits
   int nRB;          // row blocks (of 128 rows) per batch
   int nT;           // column tiles (of 128 columns) per row block
-  float2* partial;  // [batch*nRB*128][nT] per-tile row (max, sumexp), log2 domain
-  uint32_t* sync;   // [batch*nRB][kSyncWords] row-block counter and generation
-  uint32_t* err;    // [0] bit 0: a row-block wait timed out; [1] longest wait
+  float2* partial;  // split path: [batch][nRB * tile rows][nT] per-tile row (max, sumexp), log2
+  uint64_t* ent;    // exchange path: [slot][128] tagged per-row log-sum-exp entries
+  uint32_t* gen;    // exchange path: [kMaxExchangeTiles] slot generation words
+  uint32_t* err;    // [0] bit 0: an exchange wait timed out; [1] longest wait
                     // (100 MHz ticks); [2] number of timed-out waits
-  uint64_t spin_ticks;  // row-block wait limit, 100 MHz ticks
+  uint32_t* mailbox;    // host-visible word set on a timed-out wait (may be NULL)
+  uint64_t spin_ticks;  // exchange wait limit, 100 MHz ticks
 };
 
-// tile_rows: 128, or 256 for the split path with 16-bit or fp8 inputs (else NULL).
-const void* chain_kernel_symbol(int in_dt, int out_dt, int epi, int tile_rows = 128);
+// tile_rows: 128, or 256 for the split path with 16-bit or fp8 inputs; ks: 1,
+// or 2 for the k-split wave layout of 128-row tiles (exchange and split
+// epilogues, 16-bit and fp8 inputs).  NULL for a combination not built.
+const void* chain_kernel_symbol(int in_dt, int out_dt, int epi, int tile_rows = 128, int ks = 1);
 const void* rescale_kernel_symbol(int out_dt);
 // Waves that share one row in rescale_rows_kernel (its grid is rows * wpr / 4).
 int rescale_waves_per_row(int64_t rows_total, int cu_count);
 const void* zero_kernel_symbol();
-int chain_kernel_lds_bytes(int in_dt, int out_dt);
+int chain_kernel_lds_bytes(int in_dt, int out_dt, int ks = 1);
 // Tile height (128 or 256) the split path uses for this problem on a device
 // with cu_count compute units.
 int split_tile_rows(int in_dt, int64_t batch, int64_t m, int64_t n, int cu_count);
