@@ -81,6 +81,32 @@ int wtc_matmul_softmax(const void *a, const void *b, void *out, int64_t batch,
                        float scale_b, int path, void *workspace,
                        size_t workspace_bytes, void *stream);
 
+/* Size of the device scratch array behind wtc_matmul_softmax_noalloc. */
+#define WTC_NOALLOC_SCRATCH_BYTES (8u << 20)
+
+/* No counterpart in the reference: an allocation-free variant of
+ * wtc_matmul_softmax for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments, paths and results as wtc_matmul_softmax,
+ * except that the workspace is a fixed array of WTC_NOALLOC_SCRATCH_BYTES
+ * that the library holds on each GPU until the process ends (its address is
+ * looked up once per device, on the first call there).  It calls no
+ * hipMalloc, hipFree or other allocating routine, so it also creates no
+ * timeout mailbox or exchange event itself: a timed-out exchange wait is
+ * reported by the next call (or wtc_check_status) only once an allocating
+ * entry point has run on the device, and exchange calls on different
+ * streams are ordered only in that case too; the array's own diagnostic
+ * words are always read by wtc_read_error_flags(NULL, ...).  Problems whose
+ * workspace (wtc_matmul_softmax_workspace_size) exceeds the array get
+ * WTC_ERR_WORKSPACE.  Every call on a GPU shares that GPU's array: calls
+ * that overlap on one GPU (other streams, other host threads) race and must
+ * not be made. */
+int wtc_matmul_softmax_noalloc(const void *a, const void *b, void *out,
+                               int64_t batch, int64_t m, int64_t n, int64_t k,
+                               int in_dtype, int out_dtype, float logit_scale,
+                               float scale_a, float scale_b, int path,
+                               void *stream);
+
 /* Bytes of workspace wtc_matmul_softmax needs for this problem and path
  * (AUTO, EXCHANGE and SPLIT need the same amount).  Negative on bad args. */
 int64_t wtc_matmul_softmax_workspace_size(int64_t batch, int64_t m, int64_t n,
@@ -99,8 +125,9 @@ int wtc_plan(int64_t batch, int64_t m, int64_t n, int64_t k, int in_dtype,
              int64_t *grid, int *chosen_path, int64_t *workspace_bytes);
 
 /* Reads (and with clear != 0, resets) the three diagnostic words of a
- * workspace (NULL = all default workspaces of the current device, or-ed /
- * max-ed / summed) into flags[0..2]: flags[0] bit 0 = an exchange-path wait
+ * workspace (NULL = all default workspaces of the current device and the
+ * scratch array of wtc_matmul_softmax_noalloc, or-ed / max-ed / summed) into
+ * flags[0..2]: flags[0] bit 0 = an exchange-path wait
  * timed out, flags[1] = longest exchange-path wait in 100 MHz ticks,
  * flags[2] = number of timed-out waits.  Synchronises the device. */
 int wtc_read_error_flags(void *workspace, uint32_t *flags, int clear);

@@ -16,6 +16,7 @@ WTC_ERR_WORKSPACE = 2
 WTC_ERR_HIP = 3
 WTC_ERR_UNSUPPORTED = 4
 WTC_ERR_TIMEOUT = 5
+NOALLOC_SCRATCH_BYTES = 8 << 20
 
 DTYPE_F32 = 0
 DTYPE_F16 = 1
@@ -40,6 +41,9 @@ SIGNATURES = {
                                           ctypes.c_int, ctypes.c_int, ctypes.c_float,
                                           ctypes.c_float, ctypes.c_float, ctypes.c_int,
                                           _c_p, ctypes.c_size_t, _c_p]),
+    "wtc_matmul_softmax_noalloc": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64,
+                                                  ctypes.c_int, ctypes.c_int, ctypes.c_float,
+                                                  ctypes.c_float, ctypes.c_float, ctypes.c_int, _c_p]),
     "wtc_matmul_softmax_workspace_size": (_c_i64, [_c_i64, _c_i64, _c_i64, _c_i64,
                                                    ctypes.c_int, ctypes.c_int, ctypes.c_int]),
     "wtc_workspace_init": (ctypes.c_int, [_c_p, ctypes.c_size_t, _c_p]),

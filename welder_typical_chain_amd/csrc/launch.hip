@@ -213,7 +213,10 @@ int exchange_lds_pad(int in_dt, int out_dt) {
   return stat >= want ? 0 : want - stat;
 }
 
-int device_state(int dev, DeviceState** out) {
+// The device's state.  `host_objects`: also create the timeout mailbox
+// (pinned host memory) and the exchange event, which the allocation-free
+// entry point never does itself (it uses them when an earlier call made them).
+int device_state(int dev, DeviceState** out, bool host_objects = true) {
   if (dev < 0 || dev >= kMaxDevices) return fail(WTC_ERR_HIP, "device index out of range");
   DeviceState& s = g_dev[dev];
   if (!s.init) {
@@ -229,6 +232,9 @@ int device_state(int dev, DeviceState** out) {
         HIP_TRY(hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, fn, chain_kernel_threads(i), pad));
         s.occ[i][o] = nb;
       }
+    s.init = true;
+  }
+  if (host_objects && !s.mailbox_host) {
     void* mb = nullptr;
     HIP_TRY(hipHostMalloc(&mb, 64, hipHostMallocMapped | hipHostMallocCoherent));
     std::memset(mb, 0, 64);
@@ -238,7 +244,6 @@ int device_state(int dev, DeviceState** out) {
     s.mailbox_dev = static_cast<uint32_t*>(mbd);
     // ordering between streams of one device only: no system-scope fence
     HIP_TRY(hipEventCreateWithFlags(&s.exch_event, hipEventDisableTiming | hipEventDisableSystemFence));
-    s.init = true;
   }
   *out = &s;
   return WTC_OK;
@@ -331,7 +336,7 @@ int launch_tile(const void* kern, int threads, int64_t grid, int lds_dyn,
 }
 
 // A timed-out exchange wait of an earlier call on this device, reported once.
-int take_mailbox(DeviceState* ds) {
+int take_mailbox(DeviceState* ds) {  // no mailbox yet: nothing to report
   if (ds->mailbox_host && *ds->mailbox_host != 0u &&
       __atomic_exchange_n(const_cast<uint32_t*>(ds->mailbox_host), 0u, __ATOMIC_SEQ_CST) != 0u) {
     return fail(WTC_ERR_TIMEOUT,
@@ -349,7 +354,8 @@ int take_mailbox(DeviceState* ds) {
 // it, nor can the capture complete it).
 int launch_exchange(DeviceState* ds, const void* kern, int threads, int64_t grid, int lds_dyn,
                     const ChainParams& p, hipStream_t stream) {
-  if (stream_capturing(stream)) return launch_tile(kern, threads, grid, lds_dyn, p, stream);
+  if (!ds->exch_event || stream_capturing(stream))
+    return launch_tile(kern, threads, grid, lds_dyn, p, stream);
   if (ds->exch_used && stream != ds->exch_stream)
     HIP_TRY(hipStreamWaitEvent(stream, ds->exch_event, 0));
   const int rc = launch_tile(kern, threads, grid, lds_dyn, p, stream, ds->exch_event);
@@ -358,6 +364,34 @@ int launch_exchange(DeviceState* ds, const void* kern, int threads, int64_t grid
   ds->exch_stream = stream;
   return WTC_OK;
 }
+
+// ---- scratch of the allocation-free entry point ------------------------------
+// A file-scope device array, zeroed when the code object is loaded on a GPU
+// (every GPU holds its own copy until the process ends).  Host code never
+// passes `scratch` itself to a kernel or a copy: its address on a device is
+// taken once with hipGetSymbolAddress (with that device current) and kept per
+// device.  Nothing in it needs clearing between calls: the exchange path's
+// slot generation words start at zero with the array and stay consistent
+// across calls of any shape, and every other region is written before it is
+// read within a call.
+static __device__ __align__(256) uint8_t scratch[WTC_NOALLOC_SCRATCH_BYTES];
+void* g_scratch[kMaxDevices] = {};
+
+int scratch_address(int dev, void** out) {
+  if (!g_scratch[dev]) {
+    void* ptr = nullptr;
+    HIP_TRY(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+    if (!ptr) return fail(WTC_ERR_HIP, "hipGetSymbolAddress returned NULL for the scratch array");
+    g_scratch[dev] = ptr;
+  }
+  *out = g_scratch[dev];
+  return WTC_OK;
+}
+
+int matmul_softmax_impl(const void* a, const void* b, void* out, int64_t batch, int64_t m,
+                        int64_t n, int64_t k, int in_dtype, int out_dtype, float logit_scale,
+                        float scale_a, float scale_b, int path, void* workspace,
+                        size_t workspace_bytes, void* stream_, bool noalloc);
 
 }  // namespace
 
@@ -419,6 +453,7 @@ int wtc_read_error_flags(void* workspace, uint32_t* flags, int clear) {
     if (dev < 0 || dev >= kMaxDevices) return fail(WTC_ERR_HIP, "device index out of range");
     std::lock_guard<std::mutex> lk(g_mu);
     for (const StreamWorkspace& w : g_dev[dev].ws) bufs.push_back(w.ptr);
+    if (g_scratch[dev]) bufs.push_back(g_scratch[dev]);
   }
   HIP_TRY(hipDeviceSynchronize());
   for (void* b : bufs) {
@@ -438,8 +473,29 @@ int wtc_read_error_flags(void* workspace, uint32_t* flags, int clear) {
 int wtc_matmul_softmax(const void* a, const void* b, void* out, int64_t batch, int64_t m,
                        int64_t n, int64_t k, int in_dtype, int out_dtype, float logit_scale,
                        float scale_a, float scale_b, int path, void* workspace,
-                       size_t workspace_bytes, void* stream_) {
+                       size_t workspace_bytes, void* stream) {
   g_last_error.clear();
+  return matmul_softmax_impl(a, b, out, batch, m, n, k, in_dtype, out_dtype, logit_scale, scale_a,
+                             scale_b, path, workspace, workspace_bytes, stream, false);
+}
+
+int wtc_matmul_softmax_noalloc(const void* a, const void* b, void* out, int64_t batch, int64_t m,
+                               int64_t n, int64_t k, int in_dtype, int out_dtype,
+                               float logit_scale, float scale_a, float scale_b, int path,
+                               void* stream) {
+  g_last_error.clear();
+  return matmul_softmax_impl(a, b, out, batch, m, n, k, in_dtype, out_dtype, logit_scale, scale_a,
+                             scale_b, path, nullptr, 0, stream, true);
+}
+
+}  // extern "C"
+
+namespace {
+
+int matmul_softmax_impl(const void* a, const void* b, void* out, int64_t batch, int64_t m,
+                        int64_t n, int64_t k, int in_dtype, int out_dtype, float logit_scale,
+                        float scale_a, float scale_b, int path, void* workspace,
+                        size_t workspace_bytes, void* stream_, bool noalloc) {
   hipStream_t stream = static_cast<hipStream_t>(stream_);
   int rc = check_args(batch, m, n, k, in_dtype, out_dtype, path);
   if (rc) return rc;
@@ -455,7 +511,7 @@ int wtc_matmul_softmax(const void* a, const void* b, void* out, int64_t batch, i
   HIP_TRY(hipGetDevice(&dev));
   std::lock_guard<std::mutex> lk(g_mu);
   DeviceState* ds = nullptr;
-  rc = device_state(dev, &ds);
+  rc = device_state(dev, &ds, !noalloc);
   if (rc) return rc;
   rc = take_mailbox(ds);
   if (rc) return rc;
@@ -467,7 +523,16 @@ int wtc_matmul_softmax(const void* a, const void* b, void* out, int64_t batch, i
   if (rc) return rc;
 
   void* ws = workspace;
-  if (ws) {
+  if (noalloc) {
+    if (need > (int64_t)WTC_NOALLOC_SCRATCH_BYTES)
+      return fail(WTC_ERR_WORKSPACE,
+                  "this problem needs " + std::to_string(need) +
+                      " bytes of workspace; the allocation-free entry point has " +
+                      std::to_string((int64_t)WTC_NOALLOC_SCRATCH_BYTES) +
+                      " (use wtc_matmul_softmax with a workspace)");
+    rc = scratch_address(dev, &ws);
+    if (rc) return rc;
+  } else if (ws) {
     if ((int64_t)workspace_bytes < need)
       return fail(WTC_ERR_WORKSPACE, "workspace needs " + std::to_string(need) + " bytes");
     if (reinterpret_cast<uintptr_t>(ws) & 255u)
@@ -568,4 +633,4 @@ int wtc_matmul_softmax(const void* a, const void* b, void* out, int64_t batch, i
   return WTC_OK;
 }
 
-}  // extern "C"
+}  // namespace
