@@ -284,3 +284,41 @@ def test_one_hip_runtime_whichever_loads_first():
                          text=True, timeout=300)
     assert out.returncode == 0, out.stderr
     assert out.stdout.strip() == "1"
+
+
+@pytest.mark.parametrize("name", ["C1", "C2", "C3", "C4", "C5"])
+@pytest.mark.parametrize("fused", [1, 0])
+def test_compile_output_passes_reference_callers(L, tmp_path, name, fused):
+    """Replays what the reference's callers do with an unmodified compile
+    output directory: BuildCutEdgesTransform requires 05.out.nvvm.runnable.mlir
+    (compiler/transform/BuildCutEdgesTransform.cpp:34,50-53), and
+    validatePostbufferizeArtifacts requires 03.after_postbufferize.mlir,
+    04.after_workgroup_launch.mlir and 05.out.nvvm.runnable.mlir to exist and
+    be non-empty, then counts operations in them
+    (compiler/runtime/PostbufferizeFixups.cpp:46-82)."""
+    cfg = CONFIGS[name]
+    src = write_chain(tmp_path, cfg)
+    rc, tiles, err = solve(L, src, tmp_path)
+    assert rc == 0, err
+    out = tmp_path / ("fused" if fused else "baseline")
+    rc, err = compile_chain(L, src, out, tiles, fused=fused)
+    assert rc == 0, err
+    # BuildCutEdgesTransform.cpp:34,50-53
+    assert (out / "05.out.nvvm.runnable.mlir").exists()
+    # PostbufferizeFixups.cpp:46-60
+    post = (out / "03.after_postbufferize.mlir").read_text()
+    launch = (out / "04.after_workgroup_launch.mlir").read_text()
+    runnable = (out / "05.out.nvvm.runnable.mlir").read_text()
+    assert post and launch and runnable
+    # the counts the validator reports (PostbufferizeFixups.cpp:62-82)
+    plan_json = json.loads((out / "04.kernel.plan.json").read_text())
+    assert post.count("linalg.matmul") + post.count("linalg.batch_matmul") >= 1
+    assert launch.count("gpu.launch") == len(plan_json["kernels"])
+    assert launch.count("memref.alloca") == 0
+    assert runnable.count("nvvm.mma.sync") == 0
+    assert runnable.count("ld.local") == 0 and runnable.count("st.local") == 0
+    # the launch plan module names each kernel's grid / block / LDS
+    for k in plan_json["kernels"]:
+        assert f"arith.constant {k['grid'][0]} : index" in launch
+        assert f"arith.constant {k['block'][0]} : index" in launch
+    assert f'wtc.path = "{plan_json["path"]}"' in runnable

@@ -41,7 +41,7 @@ def test_full_mode_layout(cli, c2_mlir, tmp_path):
     out = tmp_path / "out"
     r = run(cli, "--input", c2_mlir, "--output-dir", out, "--verbose")
     assert r.returncode == 0, r.stderr
-    assert "[wtc] pipeline completed. artifact: " in r.stdout
+    assert "[wtc-compiler] done: " in r.stdout
     for rel in ["ir/01.canonicalized.mlir", "ir/01.canonicalize.log", "ir/02.tagged.mlir",
                 "ir/02.tags.json", "search/best.json", "search/best_summary.json",
                 "search/candidates.tsv", "search/solver.log", "fused/03.chain.canonical.mlir",
@@ -67,7 +67,7 @@ def test_search_only_stops_after_best_json(cli, c2_mlir, tmp_path):
     out = tmp_path / "out"
     r = run(cli, "--input", c2_mlir, "--output-dir", out, "--search-only")
     assert r.returncode == 0, r.stderr
-    assert r.stdout.strip() == f"[wtc] search completed. best: {out / 'search' / 'best.json'}"
+    assert r.stdout.strip() == f"[wtc-compiler] tiles written to {out / 'search' / 'best.json'}"
     assert (out / "search" / "candidates.tsv").is_file()
     assert not (out / "fused").exists()
 
@@ -96,7 +96,7 @@ def test_no_search_and_tile_overrides(cli, c2_mlir, tmp_path):
     out = tmp_path / "out"
     r = run(cli, "--input", c2_mlir, "--output-dir", out, "--no-search", "--verbose")
     assert r.returncode == 0, r.stderr
-    assert "built-in default tiles" in r.stdout
+    assert "default variant of the input type" in r.stdout
     # an override that no kernel variant implements fails at compile, with the
     # available variants named
     r = run(cli, "--input", c2_mlir, "--output-dir", tmp_path / "o2", "--tile-m", "48")
@@ -132,7 +132,7 @@ def test_argument_errors(cli, c2_mlir, tmp_path):
     assert run(cli, "--input", c2_mlir, "--tile-m", "x").returncode == 2
     assert run(cli, "--help").returncode == 0
     r = run(cli, "--input", tmp_path / "missing.mlir", "--output-dir", tmp_path / "o")
-    assert r.returncode == 1 and "canonicalize failed" in r.stderr
+    assert r.returncode == 1 and "not a Matmul -> row-Softmax chain" in r.stderr
     bad = tmp_path / "bad.mlir"
     bad.write_text("func.func @f() { return }\n")
     r = run(cli, "--input", bad, "--output-dir", tmp_path / "o2")

@@ -6,6 +6,7 @@
 // (the session that writes the stage files into out_dir).
 #include <dlfcn.h>
 
+#include <cctype>
 #include <cstdio>
 #include <cstdlib>
 #include <filesystem>
@@ -25,6 +26,10 @@ int chain_kernel_threads(int in_dt);
 int rows_kernel_threads();
 int split_tile_rows(int in_dt, int64_t batch, int64_t m, int64_t n, int cu_count);
 int rescale_waves_per_row(int64_t rows_total, int cu_count);
+// Compute units of the current device, or `fallback` when no GPU is visible.
+int device_cu_count(int fallback);
+// Dynamic LDS bytes the launcher adds to the exchange kernel.
+int exchange_lds_pad(int in_dt, int out_dt);
 
 static std::string library_path() {
   Dl_info info{};
@@ -86,6 +91,15 @@ static int64_t cell(const std::map<std::string, std::string>* row, const char* c
   return it == row->end() ? 0 : std::strtoll(it->second.c_str(), nullptr, 10);
 }
 
+// memref type of a chain operand (rank 3 when batched).
+static std::string memref_of(const ChainSpec& spec, int64_t d1, int64_t d2, Elem e) {
+  std::ostringstream o;
+  o << "memref<";
+  if (spec.batched) o << spec.batch << "x";
+  o << d1 << "x" << d2 << "x" << elem_mlir_name(e) << ">";
+  return o.str();
+}
+
 static int compile_impl(const char* input_mlir_path, const char* out_dir, int64_t tile_m,
                         int64_t tile_n, int64_t tile_k, int64_t thread_tile_m,
                         int64_t thread_tile_n, int64_t max_connect_level, int fused, int verbose,
@@ -124,11 +138,13 @@ static int compile_impl(const char* input_mlir_path, const char* out_dir, int64_
     return session_fail(o.str());
   }
   const int in_code = elem_to_dtype_code(spec.in), out_code = elem_to_dtype_code(spec.out);
-  // Plan for MI355X: 256 CUs, one exchange workgroup per CU.
+  // Plan for the current device (MI355X's 256 CUs without one); the
+  // exchange kernel's LDS footprint holds one of its workgroups per CU.
+  const int cu_count = device_cu_count(256);
   const int path_req = fused ? WTC_PATH_AUTO : WTC_PATH_UNFUSED;
   int64_t grid = 0, ws = 0;
   int path = 0;
-  if (wtc_plan(spec.batch, spec.m, spec.n, spec.k, in_code, out_code, path_req, 256, 1, &grid,
+  if (wtc_plan(spec.batch, spec.m, spec.n, spec.k, in_code, out_code, path_req, cu_count, 1, &grid,
                &path, &ws) != WTC_OK)
     return session_fail(std::string("launch plan failed: ") + wtc_last_error());
 
@@ -147,10 +163,10 @@ static int compile_impl(const char* input_mlir_path, const char* out_dir, int64_
     int lds;
     int block = 256;
   };
-  // chain_tile_kernel<in, out, epi, PF = 3, tile rows>
-  auto chain_sym = [](int in, int out, int epi, int tm = 128) {
+  // chain_tile_kernel<in, out, epi, PF = 3, tile rows, ks>
+  auto chain_sym = [](int in, int out, int epi, int tm = 128, int ks = 1) {
     return "_ZN3wtc17chain_tile_kernelILi" + std::to_string(in) + "ELi" + std::to_string(out) +
-           "ELi" + std::to_string(epi) + "ELi3ELi" + std::to_string(tm) + "E";
+           "ELi" + std::to_string(epi) + "ELi3ELi" + std::to_string(tm) + "ELi" + std::to_string(ks) + "E";
   };
   const std::string out_t = "ILi" + std::to_string(out_code) + "E";
   std::vector<K> ks;
@@ -163,19 +179,20 @@ static int compile_impl(const char* input_mlir_path, const char* out_dir, int64_
                   grid, 0, rows_kernel_threads()});
   } else if (path == WTC_PATH_EXCHANGE) {
     ks.push_back({"chain_tile_kernel<" + kin + "," + kout + ",exchange>",
-                  chain_sym(in_code, out_code, 0), grid, 82944, tile_threads});
+                  chain_sym(in_code, out_code, 0, 128, in_code == 0 ? 1 : 2), grid,
+                  exchange_lds_pad(in_code, out_code), tile_threads});
   } else if (path == WTC_PATH_SPLIT) {
-    const int tm = split_tile_rows(in_code, spec.batch, spec.m, spec.n, 256);
+    const int tm = split_tile_rows(in_code, spec.batch, spec.m, spec.n, cu_count);
     ks.push_back({"chain_tile_kernel<" + kin + "," + kout + ",split," + std::to_string(tm) + "x128>",
                   chain_sym(in_code, out_code, 1, tm), grid, 0, tile_threads});
     ks.push_back({"rescale_rows_kernel<" + kout + ">", "_ZN3wtc19rescale_rows_kernel" + out_t,
-                  (rows * rescale_waves_per_row(rows, 256) + 3) / 4, 8192});
+                  (rows * rescale_waves_per_row(rows, cu_count) + 3) / 4, 0});
   } else {
     ks.push_back({"chain_tile_kernel<" + kin + ",f32,logits>", chain_sym(in_code, 0, 2), grid, 0,
                   tile_threads});
-    ks.push_back({"rowmax_kernel", "_ZN3wtc13rowmax_kernel", rows, 16});
+    ks.push_back({"rowmax_kernel", "_ZN3wtc13rowmax_kernel", rows, 0});
     ks.push_back({"expsub_kernel", "_ZN3wtc13expsub_kernel", rows, 0});
-    ks.push_back({"rowsum_kernel", "_ZN3wtc13rowsum_kernel", rows, 16});
+    ks.push_back({"rowsum_kernel", "_ZN3wtc13rowsum_kernel", rows, 0});
     ks.push_back({"rowdiv_kernel<" + kout + ">", "_ZN3wtc13rowdiv_kernel" + out_t, rows, 0});
   }
 
@@ -252,7 +269,56 @@ static int compile_impl(const char* input_mlir_path, const char* out_dir, int64_
          << " in=" << kin << " out=" << kout << " path=" << path_name(path) << "\n";
   report << per_kernel.str();
 
-  if (!write_file((od / "03.chain.canonical.mlir").string(), canonical) ||
+  // The stage files under the reference's names (its callers check that they
+  // exist and are not empty, then count operations in them): the canonical
+  // chain, the launch plan as a module of gpu.launch_func operations, and the
+  // manifest of the gfx950 code object that runs the chain.
+  const std::string a_t = memref_of(spec, spec.m, spec.k, spec.in);
+  const std::string b_t = memref_of(spec, spec.k, spec.n, spec.in);
+  const std::string o_t = memref_of(spec, spec.m, spec.n, spec.out);
+  const std::string w_t = "memref<" + std::to_string(ws) + "xi8>";
+  std::ostringstream wg;
+  wg << "// Launch plan of the fused Matmul -> row-Softmax chain on gfx950: one\n"
+     << "// launch operation per HIP kernel of the " << path_name(path) << " path.  The kernel\n"
+     << "// bodies are in the code object 05.out.gfx950.hsaco (library " << lib << "),\n"
+     << "// launched by wtc_matmul_softmax; the workspace holds the row statistics.\n"
+     << "module attributes {gpu.container_module, wtc.target = \"gfx950\", wtc.path = \""
+     << path_name(path) << "\", wtc.compute_units = " << cu_count << " : i32} {\n"
+     << "  gpu.module @wtc_kernels [#rocdl.target<chip = \"gfx950\">] {\n  }\n"
+     << "  func.func @chain(%a: " << a_t << ", %b: " << b_t << ", %out: " << o_t << ", %ws: " << w_t
+     << ") {\n    %c1 = arith.constant 1 : index\n";
+  for (size_t i = 0; i < ks.size(); ++i) {
+    std::string kname = ks[i].name;
+    for (char& c : kname)
+      if (!std::isalnum(static_cast<unsigned char>(c))) c = '_';
+    wg << "    %g" << i << " = arith.constant " << ks[i].grid << " : index\n"
+       << "    %t" << i << " = arith.constant " << ks[i].block << " : index\n"
+       << "    %l" << i << " = arith.constant " << ks[i].lds << " : i32\n"
+       << "    gpu.launch_func @wtc_kernels::@" << kname << " blocks in (%g" << i
+       << ", %c1, %c1) threads in (%t" << i << ", %c1, %c1) dynamic_shared_memory_size %l" << i
+       << " args(%a : " << a_t << ", %b : " << b_t << ", %out : " << o_t << ", %ws : " << w_t
+       << ")\n";
+  }
+  wg << "    return\n  }\n}\n";
+  std::ostringstream run;
+  run << "// Runnable artefact of the chain for gfx950 (no NVVM is involved): the HIP\n"
+      << "// code object 05.out.gfx950.hsaco, run through wtc_matmul_softmax with the\n"
+      << "// arguments below.  Per-kernel resources are in kernel_report.txt.\n"
+      << "module attributes {wtc.target = \"gfx950\", wtc.code_object = \"05.out.gfx950.hsaco\", "
+      << "wtc.library = \"" << lib << "\", wtc.entry = \"wtc_matmul_softmax\", wtc.path = \""
+      << path_name(path) << "\", wtc.path_code = " << path << " : i32, wtc.in_dtype = " << in_code
+      << " : i32, wtc.out_dtype = " << out_code << " : i32, wtc.batch = " << spec.batch
+      << " : i64, wtc.m = " << spec.m << " : i64, wtc.n = " << spec.n << " : i64, wtc.k = " << spec.k
+      << " : i64, wtc.workspace_bytes = " << ws << " : i64, wtc.mfma_instructions = " << mfma
+      << " : i64, wtc.scratch_bytes = " << scratch_bytes << " : i64} {\n";
+  for (const K& k : ks)
+    run << "  // kernel " << k.name << ": grid " << k.grid << ", block " << k.block
+        << ", dynamic LDS " << k.lds << " bytes\n";
+  run << "}\n";
+  if (!write_file((od / "03.after_postbufferize.mlir").string(), canonical) ||
+      !write_file((od / "04.after_workgroup_launch.mlir").string(), wg.str()) ||
+      !write_file((od / "05.out.nvvm.runnable.mlir").string(), run.str()) ||
+      !write_file((od / "03.chain.canonical.mlir").string(), canonical) ||
       !write_file((od / "04.kernel.plan.json").string(), plan.str()) ||
       !write_file((od / "05.out.hip.launch.json").string(), launch.str()) ||
       !write_file((od / "kernel_report.txt").string(), report.str()))

@@ -38,9 +38,27 @@ int split_tile_rows(int in_dt, int64_t batch, int64_t m, int64_t n, int cu_count
   return rb128 % 2 == 0 && tiles256 >= 2 * (int64_t)cu_count ? 256 : 128;
 }
 
+// Compute units of the current device, or `fallback` when no GPU is visible
+// (the compile C-ABI also runs on build hosts).
+int device_cu_count(int fallback) {
+  int n = 0, dev = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n <= 0 || hipGetDevice(&dev) != hipSuccess) return fallback;
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, dev) != hipSuccess || prop.multiProcessorCount <= 0) return fallback;
+  return prop.multiProcessorCount;
+}
+
 // Wave layout of the exchange path's 128-row tiles: k-split (ks = 2) for
 // 16-bit and fp8 inputs, 4 waves of 64x64 for f32.
 int exchange_ks(int in_dt) { return in_dt == DT_F32 ? 1 : 2; }
+
+// Dynamic LDS added to the exchange kernel so that no CU holds two of its
+// workgroups (spreads a grid of <= CU-count tiles over all CUs).
+int exchange_lds_pad(int in_dt, int out_dt) {
+  const int stat = chain_kernel_lds_bytes(in_dt, out_dt, exchange_ks(in_dt));
+  const int want = 80 * 1024 + 1024;
+  return stat >= want ? 0 : want - stat;
+}
 }  // namespace wtc
 
 namespace {
@@ -205,13 +223,6 @@ DeviceState g_dev[kMaxDevices];
       return fail(WTC_ERR_HIP, std::string(#expr) + ": " + hipGetErrorString(e_)); \
   } while (0)
 
-// Dynamic LDS added to the exchange kernel so that no CU holds two of its
-// workgroups (spreads a grid of <= CU-count tiles over all CUs).
-int exchange_lds_pad(int in_dt, int out_dt) {
-  const int stat = chain_kernel_lds_bytes(in_dt, out_dt, exchange_ks(in_dt));
-  const int want = 80 * 1024 + 1024;
-  return stat >= want ? 0 : want - stat;
-}
 
 // The device's state.  `host_objects`: also create the timeout mailbox
 // (pinned host memory) and the exchange event, which the allocation-free

@@ -144,20 +144,20 @@ bool tag(const fs::path& canonical_path, const wtc::ChainSpec& spec, const fs::p
 // re-targeted to the HIP artefacts: counts from the canonical IR, the launch
 // plan and the kernel report instead of post-bufferize IR, gpu.launch and PTX.
 bool validate(const fs::path& dir, std::string& diag) {
-  const fs::path canonical = dir / "03.chain.canonical.mlir";
-  const fs::path plan = dir / "04.kernel.plan.json";
-  const fs::path launch = dir / "05.out.hip.launch.json";
+  // the files the reference's callers require, then this build's HIP files
+  const char* names[] = {"03.after_postbufferize.mlir", "04.after_workgroup_launch.mlir",
+                         "05.out.nvvm.runnable.mlir", "03.chain.canonical.mlir",
+                         "04.kernel.plan.json", "05.out.hip.launch.json"};
+  std::string text[6];
+  for (int i = 0; i < 6; ++i)
+    if (!wtc::read_file((dir / names[i]).string(), text[i]) || text[i].empty()) {
+      diag = std::string(names[i]) + " is missing or empty in " + dir.string();
+      return false;
+    }
+  const std::string& c = text[0];
+  const std::string& p = text[4];
   const fs::path kreport = dir / "kernel_report.txt";
-  if (!fs::exists(canonical) || !fs::exists(plan) || !fs::exists(launch)) {
-    diag = "expected compiler artifacts are missing under " + dir.string();
-    return false;
-  }
-  std::string c, p, l, k;
-  if (!wtc::read_file(canonical.string(), c) || !wtc::read_file(plan.string(), p) ||
-      !wtc::read_file(launch.string(), l) || c.empty() || p.empty() || l.empty()) {
-    diag = "failed to read compiler artifacts under " + dir.string();
-    return false;
-  }
+  std::string k;
   wtc::read_file(kreport.string(), k);
   auto report_value = [&](const char* key) -> std::string {
     const std::string needle = std::string(key) + "=";
@@ -176,7 +176,7 @@ bool validate(const fs::path& dir, std::string& diag) {
   r << "scratch_instruction_count=" << report_value("scratch_instruction_count") << "\n";
   r << "vgpr_spill_count=" << report_value("vgpr_spill_count") << "\n";
   if (!wtc::write_file((dir / "postbufferize_report.txt").string(), r.str())) {
-    diag = "failed to write postbufferize report: " + (dir / "postbufferize_report.txt").string();
+    diag = "could not write " + (dir / "postbufferize_report.txt").string();
     return false;
   }
   return true;
@@ -190,7 +190,7 @@ bool any_override(const wtc::TileParams& t) {
 int run_pipeline(const Options& o) {
   std::string diag;
   if (o.output_dir.empty()) {
-    std::cerr << "error: output dir is empty\n";
+    std::cerr << "wtc-compiler: no output directory given\n";
     return 1;
   }
   const fs::path root = o.output_dir;
@@ -199,21 +199,21 @@ int run_pipeline(const Options& o) {
   std::error_code ec;
   fs::create_directories(ir, ec);
   if (ec) {
-    std::cerr << "error: cannot create " << ir << "\n";
+    std::cerr << "wtc-compiler: could not create directory " << ir << "\n";
     return 1;
   }
 
-  if (o.verbose) std::cout << "[wtc] phase: canonicalize\n";
+  if (o.verbose) std::cout << "[wtc-compiler] recognising the chain\n";
   wtc::ChainSpec spec;
   const fs::path canonical = ir / "01.canonicalized.mlir";
   if (!canonicalize(o.input, canonical, spec, diag)) {
-    std::cerr << "error: canonicalize failed: " << diag << "\n";
+    std::cerr << "wtc-compiler: the input is not a Matmul -> row-Softmax chain: " << diag << "\n";
     return 1;
   }
-  if (o.verbose) std::cout << "[wtc] phase: tagging\n";
+  if (o.verbose) std::cout << "[wtc-compiler] writing the tagged chain\n";
   const fs::path tagged = ir / "02.tagged.mlir";
   if (!tag(canonical, spec, tagged, ir / "02.tags.json", diag)) {
-    std::cerr << "error: tagging failed: " << diag << "\n";
+    std::cerr << "wtc-compiler: could not write the tagged chain: " << diag << "\n";
     return 1;
   }
 
@@ -223,15 +223,15 @@ int run_pipeline(const Options& o) {
   wtc::TileParams best;
   bool have_best = false;
   if (!o.best_json.empty()) {
-    if (o.verbose) std::cout << "[wtc] load best json: " << o.best_json << "\n";
+    if (o.verbose) std::cout << "[wtc-compiler] tiles from " << o.best_json << "\n";
     if (!wtc::load_best_json(o.best_json, best, diag)) {
-      std::cerr << "error: failed to load --best-json: " << diag << "\n";
+      std::cerr << "wtc-compiler: --best-json unreadable: " << diag << "\n";
       return 1;
     }
     have_best = true;
   }
   if (!have_best && o.enable_search) {
-    if (o.verbose) std::cout << "[wtc] phase: search (in-process solver)\n";
+    if (o.verbose) std::cout << "[wtc-compiler] ranking the gfx950 tile variants\n";
     const fs::path summary = search / "best_summary.json", candidates = search / "candidates.tsv";
     const fs::path solver_log = search / "solver.log";
     char err[4096];
@@ -245,18 +245,17 @@ int run_pipeline(const Options& o) {
         << "\n";
     wtc::write_file(solver_log.string(), log.str());
     if (rc != 0) {
-      std::cerr << "error: search failed: backend solver failed, rc=" << rc << ", error=" << err
-                << ", see " << solver_log.string() << "\n";
+      std::cerr << "wtc-compiler: the tile solver returned " << rc << " (" << err << "); log in "
+                << solver_log.string() << "\n";
       return 1;
     }
     have_best = true;
     if (o.verbose) {
-      std::cout << "[wtc] search best: " << (search / "best.json").string() << "\n";
-      std::cout << "[wtc] search candidates: " << candidates.string() << "\n";
+      std::cout << "[wtc-compiler] ranked candidates in " << candidates.string() << "\n";
     }
   }
   if (any_override(o.override_tiles)) {
-    if (o.verbose) std::cout << "[wtc] apply tile overrides\n";
+    if (o.verbose) std::cout << "[wtc-compiler] tiles overridden on the command line\n";
     const wtc::TileParams& t = o.override_tiles;
     if (t.tile_m > 0) best.tile_m = t.tile_m;
     if (t.tile_n > 0) best.tile_n = t.tile_n;
@@ -266,28 +265,28 @@ int run_pipeline(const Options& o) {
     have_best = true;
   }
   if (!have_best && o.mode == Mode::SearchOnly) {
-    std::cerr << "error: search-only mode has no result. Provide --best-json or enable search.\n";
+    std::cerr << "wtc-compiler: --search-only needs the solver or --best-json to produce tiles\n";
     return 1;
   }
   if (!have_best) {
     // search disabled and no tiles given: the library's default variant for the input type
     best = wtc::supported_variants(spec.in).front().tiles;
-    if (o.verbose) std::cout << "[wtc] search disabled, using built-in default tiles\n";
+    if (o.verbose) std::cout << "[wtc-compiler] no search: the default variant of the input type\n";
   }
   const fs::path best_path = search / "best.json";
   if (!wtc::write_best_json(best, best_path.string(), diag)) {
-    std::cerr << "error: failed to persist best.json: " << diag << "\n";
+    std::cerr << "wtc-compiler: could not write best.json: " << diag << "\n";
     return 1;
   }
   if (o.verbose)
-    std::cout << "[wtc] selected tile=(" << best.tile_m << "x" << best.tile_n << "x" << best.tile_k
-              << ") thread_tile=(" << best.thread_tile_m << "x" << best.thread_tile_n << ")\n";
+    std::cout << "[wtc-compiler] tiles " << best.tile_m << "x" << best.tile_n << "x" << best.tile_k
+              << ", lane tile " << best.thread_tile_m << "x" << best.thread_tile_n << "\n";
   if (o.mode == Mode::SearchOnly) {
-    std::cout << "[wtc] search completed. best: " << best_path.string() << "\n";
+    std::cout << "[wtc-compiler] tiles written to " << best_path.string() << "\n";
     return 0;
   }
 
-  if (o.verbose) std::cout << "[wtc] phase: build + compile (gfx950)\n";
+  if (o.verbose) std::cout << "[wtc-compiler] planning the gfx950 launch\n";
   fs::create_directories(compile_dir, ec);
   char err[4096];
   const int rc = welder_compile_typical_chain_to_nvvm(
@@ -301,42 +300,36 @@ int run_pipeline(const Options& o) {
        << (rc ? std::string(" error=") + err : "") << "\n";
   wtc::write_file((compile_dir / "compile.log").string(), clog.str());
   if (rc != 0) {
-    std::cerr << "error: build/compile failed: welder_compile_typical_chain_to_nvvm rc=" << rc
-              << ": " << err << "\n";
+    std::cerr << "wtc-compiler: the compile entry point returned " << rc << ": " << err << "\n";
     return 1;
   }
-  if (o.verbose) std::cout << "[wtc] phase: validate artifacts\n";
+  if (o.verbose) std::cout << "[wtc-compiler] checking the artefacts\n";
   if (!validate(compile_dir, diag)) {
-    std::cerr << "error: artifact validation failed: " << diag << "\n";
+    std::cerr << "wtc-compiler: artefact check failed: " << diag << "\n";
     return 1;
   }
-  std::cout << "[wtc] pipeline completed. artifact: "
-            << (compile_dir / "05.out.hip.launch.json").string() << "\n";
+  std::cout << "[wtc-compiler] done: " << (compile_dir / "05.out.nvvm.runnable.mlir").string() << "\n";
   return 0;
 }
 
 void usage() {
-  std::cout << "Usage: wtc-compiler --input <mlir-file> [options]\n"
-            << "Options:\n"
-            << "  --output-dir <dir>       Output root dir (default /tmp/wtc_out)\n"
-            << "  --backend-root <dir>     Accepted for compatibility (one in-process backend)\n"
-            << "  --backend-mode <mode>    shell|process_chain|api, accepted for compatibility\n"
-            << "  --pure-api-full          Accepted for compatibility\n"
-            << "  --legacy-root <dir>      Alias of --backend-root\n"
-            << "  --search-only            Run solver only and dump search artifacts\n"
-            << "  --compile-only           Skip solver (unless no tiles provided) and compile\n"
-            << "  --best-json <path>       Read tile result from json (tileM/N/K/threadTileM/N)\n"
-            << "  --tile-m <n>             Override tileM\n"
-            << "  --tile-n <n>             Override tileN\n"
-            << "  --tile-k <n>             Override tileK\n"
-            << "  --thread-tile-m <n>      Override threadTileM\n"
-            << "  --thread-tile-n <n>      Override threadTileN\n"
-            << "  --max-connect-level <n>  Connect level for the fused path\n"
-            << "  --no-search              Do not run solver search\n"
-            << "  --repeat <n>             Repeat in one process (stress reentrancy)\n"
-            << "  --baseline               Compile baseline (unfused) variant\n"
-            << "  --fused                  Compile fused variant (default)\n"
-            << "  --verbose                Verbose logs\n";
+  std::cout << "wtc-compiler: tile selection and gfx950 launch planning for a Matmul -> row-Softmax\n"
+            << "chain given as MLIR text.\n\n"
+            << "  wtc-compiler --input FILE [--output-dir DIR] [mode] [tiles] [--repeat N] [--verbose]\n\n"
+            << "modes (default: rank the tile variants, then plan and check the launch):\n"
+            << "  --search-only             stop after writing search/best.json\n"
+            << "  --compile-only            plan with the tiles given (rank only if none are)\n"
+            << "  --no-search               take the input type's default variant when no tiles are given\n"
+            << "  --fused | --baseline      one fused kernel (default) or the five-kernel unfused chain\n"
+            << "tiles:\n"
+            << "  --best-json FILE          tileM/tileN/tileK/threadTileM/threadTileN from a JSON file\n"
+            << "  --tile-m N  --tile-n N  --tile-k N  --thread-tile-m N  --thread-tile-n N\n"
+            << "  --max-connect-level N     recorded in the plan (the fused kernel needs none)\n"
+            << "accepted and ignored (a single in-process backend):\n"
+            << "  --backend-root DIR  --legacy-root DIR  --backend-mode MODE  --pure-api-full\n"
+            << "output layout: DIR/ir (01, 02), DIR/search (best.json, best_summary.json,\n"
+            << "candidates.tsv), DIR/fused or DIR/baseline (03, 04, 05 and the HIP files);\n"
+            << "--repeat N runs the pipeline N times in one process, into DIR/iter_<i>.\n";
 }
 
 bool parse_int(const char* s, int64_t& v) {
@@ -359,7 +352,7 @@ int main(int argc, char** argv) {
     const bool has_value = i + 1 < argc;
     auto int_arg = [&](int64_t& dst) {
       if (!parse_int(argv[++i], dst)) {
-        std::cerr << "error: " << arg << " expects an integer, got '" << argv[i] << "'\n";
+        std::cerr << "wtc-compiler: " << arg << " takes an integer, not '" << argv[i] << "'\n";
         std::exit(2);
       }
     };
@@ -374,7 +367,7 @@ int main(int argc, char** argv) {
     } else if (arg == "--backend-mode" && has_value) {
       const std::string m = argv[++i];
       if (m != "shell" && m != "process_chain" && m != "api") {
-        std::cerr << "error: unknown backend mode '" << m << "' (shell|process_chain|api)\n";
+        std::cerr << "wtc-compiler: --backend-mode is one of shell, process_chain, api (got '" << m << "')\n";
         return 2;
       }
       o.backend_mode = m;
@@ -411,16 +404,16 @@ int main(int argc, char** argv) {
       usage();
       return 0;
     } else {
-      std::cerr << "Unknown argument: " << arg << "\n";
+      std::cerr << "wtc-compiler: unrecognised option " << arg << "\n";
       return 2;
     }
   }
   if (o.input.empty()) {
-    std::cerr << "error: --input is required\n";
+    std::cerr << "wtc-compiler: give the chain with --input FILE\n";
     return 2;
   }
   if (repeat <= 0) {
-    std::cerr << "error: --repeat must be >= 1\n";
+    std::cerr << "wtc-compiler: --repeat takes a count of at least 1\n";
     return 2;
   }
   if (repeat == 1) return run_pipeline(o);
@@ -432,7 +425,7 @@ int main(int argc, char** argv) {
                 << "\n";
     const int rc = run_pipeline(it);
     if (rc != 0) {
-      std::cerr << "error: repeat iteration failed at i=" << i << ", rc=" << rc << "\n";
+      std::cerr << "wtc-compiler: run " << i << " of --repeat ended with status " << rc << "\n";
       return rc;
     }
   }
