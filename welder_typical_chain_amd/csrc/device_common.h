@@ -101,6 +101,14 @@ template <> __device__ inline void pack4<DT_BF16>(const f32x4& x, uint32_t* w0, 
 }
 
 __device__ inline float wave_xor32_max(float x) { return fmaxf(x, __shfl_xor(x, 32)); }
+
+// Value of lane quad_perm(CTRL) of this lane's quad (DPP quad permute, no LDS
+// round trip): 0xB1 swaps lanes 0<->1 and 2<->3 (xor 1), 0x4E swaps the
+// pairs (xor 2).  Every lane of the wave must be active.
+template <int CTRL>
+__device__ inline float dpp_quad(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, true));
+}
 __device__ inline float wave_xor32_sum(float x) { return x + __shfl_xor(x, 32); }
 
 

@@ -551,7 +551,9 @@ __device__ inline float2 load_stat(const float2* p) {
 // entry carries the expected tag; otherwise the wave sleeps briefly and
 // reloads only the half-slots not yet done.  Polling with wide, contiguous
 // loads keeps the traffic of the waits small, and there is no round trip
-// between learning that the data is there and loading it.
+// between learning that the data is there and loading it (the counter
+// barrier this replaces needed four: statistics stores acknowledged, counter
+// update, generation store, statistics loads).
 //
 // Every wait is bounded by spin_ticks of the 100 MHz clock; a wait that runs
 // out sets bit 0 of err[0], counts in err[2], sets the caller's host-visible
@@ -879,11 +881,13 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
     float tm = wstat[r].x;
 #pragma unroll
     for (int w = 1; w < WN; ++w) tm = fmaxf(tm, wstat[w * BM + r].x);
+    // tm is finite (every tile has a column inside N); a wave whose columns
+    // all lie past N has max -inf and sum 0, and exp2(-inf) = 0
     float ts = 0.0f;
 #pragma unroll
     for (int w = 0; w < WN; ++w) {
       const float2 e = wstat[w * BM + r];
-      ts += e.x == -INFINITY ? 0.0f : e.y * __builtin_amdgcn_exp2f(e.x - tm);
+      ts += e.y * __builtin_amdgcn_exp2f(e.x - tm);
     }
     return make_float2(tm, ts);
   };
@@ -906,6 +910,11 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
         const float lse = st.x + __builtin_amdgcn_logf(st.y);
         tlse[t] = lse;
         if (!solo) store_entry(p.ent + (uint64_t)own_slot * BM + t, lse, sgen[nt] + 1u);
+        // Wait until the entry stores are acknowledged.  Not for ordering --
+        // the tags make every entry self-describing -- but measured: without
+        // the wait, entries became visible to the other XCDs late on some
+        // MI355X boxes (the exchange took 2-4 us longer), with it never.
+        __builtin_amdgcn_s_waitcnt(0);
       } else {
         // split: per-tile (max, sumexp) for the rescale kernel
         store_stat(p.partial + ((int64_t)rbg * BM + t) * p.nT + nt, st.x, st.y);
@@ -998,27 +1007,38 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
         const int part = (nT + P - 1) / P;
         const int q0 = h * part < nT ? h * part : nT;
         const int q1 = q0 + part < nT ? q0 + part : nT;
-        for (int q = q0; q < q1; ++q) {
-          const float Lq = q == (int)nt ? tlse[r] : lse_all[q * kLsePitch + r];
-          const float nm = fmaxf(gm, Lq);
-          gs = (gm == -INFINITY ? 0.0f : gs * __builtin_amdgcn_exp2f(gm - nm)) +
-               __builtin_amdgcn_exp2f(Lq - nm);
+        for (int qb = q0; qb < q1; qb += 4) {  // four independent table reads at a time
+          float l[4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const int q = qb + u;
+            l[u] = q >= q1 ? -INFINITY : (q == (int)nt ? tlse[r] : lse_all[q * kLsePitch + r]);
+          }
+          const float nm = fmaxf(gm, fmaxf(fmaxf(l[0], l[1]), fmaxf(l[2], l[3])));  // finite
+          float cs = gm == -INFINITY ? 0.0f : gs * __builtin_amdgcn_exp2f(gm - nm);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) cs += __builtin_amdgcn_exp2f(l[u] - nm);
           gm = nm;
+          gs = cs;
         }
       }
-      // gm == -inf only for an empty share; its sum is 0
+      // The P threads of row r are P consecutive lanes of one quad: combine
+      // with DPP quad permutes (xor 1, then xor 2).  gm == -inf only for an
+      // empty share; its sum is 0.
 #pragma unroll
       for (int off = 1; off < P; off <<= 1) {
-        const float om = __shfl_xor(gm, off), os = __shfl_xor(gs, off);
+        const float om = off == 1 ? dpp_quad<0xB1>(gm) : dpp_quad<0x4E>(gm);
+        const float os = off == 1 ? dpp_quad<0xB1>(gs) : dpp_quad<0x4E>(gs);
         const float M = fmaxf(gm, om);
         gs = (gm == -INFINITY ? 0.0f : gs * __builtin_amdgcn_exp2f(gm - M)) +
              (om == -INFINITY ? 0.0f : os * __builtin_amdgcn_exp2f(om - M));
         gm = M;
       }
       // thread (r, h) owns the factor of row r, column slice of wave h:
-      // exp2(m_w - max) / sum, with (max, sum) over the whole row
+      // exp2(m_w - L) with L = max + log2(sum) the row's log-sum-exp
+      const float row_lse = gm + __builtin_amdgcn_logf(gs);
       const float mw = wstat[h * BM + r].x;
-      factor[h * BM + r] = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - gm) / gs;
+      factor[h * BM + r] = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - row_lse);
     } else {
       // split: exponentials relative to the tile max, as the statistics say
       const float mw = wstat[h * BM + r].x;
