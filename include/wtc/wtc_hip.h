@@ -59,10 +59,9 @@ extern "C" {
 #define WTC_DTYPE_FP8_E4M3 3 /* OCP e4m3 ("fn"), inputs only */
 
 /* Execution paths. */
-#define WTC_PATH_AUTO 0      /* ROWS for 16-bit inputs with k <= 128 when there are at
-                                least as many row blocks as compute units or the tiles
-                                cannot all be co-resident; else EXCHANGE when every
-                                tile is co-resident; else SPLIT */
+#define WTC_PATH_AUTO 0      /* the fused path and kernel variant that the library's
+                                cost model (calibrated on MI355X) ranks fastest for
+                                the problem: EXCHANGE, SPLIT or ROWS */
 #define WTC_PATH_EXCHANGE 1  /* one kernel, row statistics exchanged between tiles */
 #define WTC_PATH_SPLIT 2     /* two kernels: tile pass + row rescale (online two-pass) */
 #define WTC_PATH_UNFUSED 3   /* five kernels: matmul, max, exp, sum, divide */
@@ -80,6 +79,38 @@ int wtc_matmul_softmax(const void *a, const void *b, void *out, int64_t batch,
                        int out_dtype, float logit_scale, float scale_a,
                        float scale_b, int path, void *workspace,
                        size_t workspace_bytes, void *stream);
+
+/* Tile parameters of one kernel variant, in the fields and units of the
+ * reference's best.json (compiler/scheduler/Search.cpp:62-86): a tile_m x
+ * tile_n output tile per workgroup, tile_k elements of K per pipeline stage,
+ * thread_tile_m x thread_tile_n accumulators per lane. */
+typedef struct wtc_tiles {
+  int64_t tile_m, tile_n, tile_k, thread_tile_m, thread_tile_n;
+} wtc_tiles;
+
+/* wtc_matmul_softmax on exactly the kernel variant `tiles` (NULL: the
+ * variant the cost model ranks first, as wtc_matmul_softmax does).  Replaces
+ * the reference's launch of the kernel it generated for best.json's tiles
+ * (welder_compile_typical_chain_to_nvvm's tile arguments,
+ * backend/welder/compiler/driver/WelderCompileCAPI.h:19-25, launched by
+ * WelderProfiler.cpp:752-792): here the variant is chosen among the built
+ * ones at call time.  With path AUTO the variant runs the fused path the
+ * cost model ranks first for it.  WTC_ERR_UNSUPPORTED when no variant has
+ * these tiles for in_dtype, or when the variant cannot run `path` for this
+ * problem (wtc_last_error says why). */
+int wtc_matmul_softmax_tiles(const void *a, const void *b, void *out, int64_t batch,
+                             int64_t m, int64_t n, int64_t k, int in_dtype,
+                             int out_dtype, float logit_scale, float scale_a,
+                             float scale_b, const wtc_tiles *tiles, int path,
+                             void *workspace, size_t workspace_bytes, void *stream);
+
+/* The kernel variants built for an input type, the candidates the solver
+ * ranks (the reference's tile space, WelderSolverSolveEntrypoints.h:157-265).
+ * Writes up to `capacity` entries -- tiles, a bit (1 << WTC_PATH_x) per
+ * path the variant runs, a static name (any array may be NULL) -- and
+ * returns the number of variants, or -1 for an unknown dtype. */
+int wtc_list_variants(int in_dtype, wtc_tiles *tiles, unsigned *paths,
+                      const char **names, int capacity);
 
 /* Size of the device scratch array behind wtc_matmul_softmax_noalloc. */
 #define WTC_NOALLOC_SCRATCH_BYTES (8u << 20)
@@ -123,6 +154,16 @@ int wtc_workspace_init(void *workspace, size_t workspace_bytes, void *stream);
 int wtc_plan(int64_t batch, int64_t m, int64_t n, int64_t k, int in_dtype,
              int out_dtype, int path, int cu_count, int wg_per_cu,
              int64_t *grid, int *chosen_path, int64_t *workspace_bytes);
+
+/* wtc_plan for one variant (`tiles`; NULL = every variant): the variant and
+ * path the cost model ranks first (for path AUTO, among the fused paths),
+ * its grid, its workspace bytes and the model's estimate of microseconds
+ * per back-to-back call.  Any output pointer may be NULL.  Pure host
+ * arithmetic (no GPU needed). */
+int wtc_plan_tiles(int64_t batch, int64_t m, int64_t n, int64_t k, int in_dtype,
+                   int out_dtype, int path, const wtc_tiles *tiles, int cu_count,
+                   int wg_per_cu, wtc_tiles *chosen_tiles, int *chosen_path,
+                   int64_t *grid, int64_t *workspace_bytes, double *estimated_us);
 
 /* Reads (and with clear != 0, resets) the three diagnostic words of a
  * workspace (NULL = all default workspaces of the current device and the

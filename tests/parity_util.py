@@ -54,7 +54,7 @@ def to_device(raw: np.ndarray, in_dtype: str, device="cuda") -> torch.Tensor:
 
 
 def run_chain(inp: O.ChainInputs, in_dtype: str, out_dtype: str, path: str = "auto",
-              batched: bool | None = None, workspace=None) -> torch.Tensor:
+              batched: bool | None = None, workspace=None, tiles=None) -> torch.Tensor:
     from welder_typical_chain_amd.chain import matmul_softmax
     a = to_device(inp.a_raw, in_dtype)
     b = to_device(inp.b_raw, in_dtype)
@@ -64,7 +64,7 @@ def run_chain(inp: O.ChainInputs, in_dtype: str, out_dtype: str, path: str = "au
         a, b = a[0], b[0]
     out = matmul_softmax(a, b, out_dtype=_TORCH_OUT[out_dtype], logit_scale=inp.logit_scale,
                          scale_a=inp.scale_a, scale_b=inp.scale_b, path=path,
-                         workspace=workspace)
+                         workspace=workspace, tiles=tiles)
     torch.cuda.synchronize()
     return out
 

@@ -82,15 +82,10 @@ def test_plan_headline_and_configs(L):
     # C4: 256 column tiles per row -> split, with 256-row tiles (4 x 256)
     rc, grid, path, _ = plan(L, 1, 1024, 32768, 4096, _lib.DTYPE_BF16, 1, _lib.PATH_AUTO)
     assert (rc, grid, path) == (0, 4 * 256, _lib.PATH_SPLIT)
-    # C5 (fp8): 32 x 64 256-row tiles
-    assert plan(L, 1, 8192, 8192, 4096, _lib.DTYPE_FP8_E4M3, 1, _lib.PATH_AUTO)[:3] == \
-        (0, 32 * 64, _lib.PATH_SPLIT)
-    # 256-row tiles only for an even number of 128-row blocks and >= 2 tiles per
-    # CU, never for f32: otherwise 128-row tiles
-    assert plan(L, 1, 1152, 32768, 4096, _lib.DTYPE_BF16, 1, _lib.PATH_SPLIT)[1] == 9 * 256
-    assert plan(L, 1, 256, 32768, 64, _lib.DTYPE_BF16, 1, _lib.PATH_SPLIT)[1] == 2 * 256
+    # C5 (fp8): split (128-row k-split tiles measure within 1.3 % of 256-row ones)
+    assert plan(L, 1, 8192, 8192, 4096, _lib.DTYPE_FP8_E4M3, 1, _lib.PATH_AUTO)[2] == _lib.PATH_SPLIT
+    # f32 has one layout (128-row tiles)
     assert plan(L, 1, 1024, 32768, 64, _lib.DTYPE_F32, 0, _lib.PATH_SPLIT)[1] == 8 * 256
-    assert plan(L, 64, 200, 1000, 72, _lib.DTYPE_F16, 1, _lib.PATH_SPLIT)[1] == 64 * 8
     # forcing the exchange path where it cannot be co-resident is refused
     rc, *_ = plan(L, 1, 1024, 32768, 4096, _lib.DTYPE_BF16, 1, _lib.PATH_EXCHANGE)
     assert rc == _lib.WTC_ERR_UNSUPPORTED and b"co-resident" in L.wtc_last_error()
@@ -100,6 +95,92 @@ def test_plan_headline_and_configs(L):
     # unfused needs room for the f32 logits
     _, _, _, ws_u = plan(L, 1, 2048, 2048, 1024, 1, 1, _lib.PATH_UNFUSED)
     assert ws_u >= ws + 2048 * 2048 * 4
+
+
+F16, BF16, FP8, F32 = _lib.DTYPE_F16, _lib.DTYPE_BF16, _lib.DTYPE_FP8_E4M3, _lib.DTYPE_F32
+T128 = {F16: [128, 128, 64, 2, 16], BF16: [128, 128, 64, 2, 16], FP8: [128, 128, 128, 2, 16]}
+KS2 = {F16: [128, 128, 64, 2, 32], BF16: [128, 128, 64, 2, 32], FP8: [128, 128, 128, 2, 32]}
+T256 = {F16: [256, 128, 64, 2, 32], BF16: [256, 128, 64, 2, 32], FP8: [256, 128, 128, 2, 32]}
+ROWS = [128, 128, 128, 2, 16]
+
+
+def test_variant_table(L):
+    """Four variants for 16-bit inputs, three for fp8 (no rows kernel), one
+    for f32; tiles distinct within an input type; each runs the paths its
+    kernels implement."""
+    ex, sp, un, ro = (1 << _lib.PATH_EXCHANGE, 1 << _lib.PATH_SPLIT, 1 << _lib.PATH_UNFUSED,
+                      1 << _lib.PATH_ROWS)
+    for dt in (F16, BF16):
+        vs = _lib.variants(dt)
+        assert [v[1] for v in vs] == [T128[dt], KS2[dt], T256[dt], ROWS]
+        assert [v[2] for v in vs] == [ex | sp | un, ex | sp | un, sp | un, ro]
+    assert [v[1] for v in _lib.variants(FP8)] == [T128[FP8], KS2[FP8], T256[FP8]]
+    assert [v[1] for v in _lib.variants(F32)] == [[128, 128, 32, 2, 32]]
+    assert len({v[0] for dt in (F16, FP8, F32) for v in _lib.variants(dt)}) == 5
+    assert L.wtc_list_variants(9, None, None, None, 0) == -1
+
+
+# Shapes of the calibration sweep (welder_typical_chain_amd/calibrate.py)
+# where the cost model picks the measured fastest (variant, path) on MI355X
+# (back-to-back calls); tests/test_cost_model.py scores every shape.
+MEASURED_BEST = [
+    ((1, 2048, 2048, 1024, F16, F16), KS2[F16], _lib.PATH_EXCHANGE),   # C2: 15.8 vs 16.3 us
+    ((1, 2048, 2048, 64, F16, F16), T128[F16], _lib.PATH_EXCHANGE),    # 8.1 vs 8.9
+    ((1, 2048, 2048, 256, F16, F16), T128[F16], _lib.PATH_EXCHANGE),   # 9.7 vs 9.9
+    ((1, 8192, 128, 64, F16, F16), T128[F16], _lib.PATH_EXCHANGE),     # 5.6 vs rows 7.2
+    ((1, 4096, 4096, 1024, F16, F16), T256[F16], _lib.PATH_SPLIT),     # 64.9 vs 73.6
+    ((1, 2048, 8192, 512, F16, F16), T256[F16], _lib.PATH_SPLIT),      # 52.6 vs 65.0
+    ((8, 2048, 2048, 128, F16, F16), ROWS, _lib.PATH_ROWS),            # 50.2 vs split 57.1
+    ((16, 512, 512, 64, F16, F16), T128[F16], _lib.PATH_EXCHANGE),     # 7.6 vs rows 15.8
+    ((1, 4096, 2048, 128, F16, F16), T256[F16], _lib.PATH_SPLIT),      # 22.2 vs rows 49.0
+    ((64, 2048, 2048, 128, F16, F16), ROWS, _lib.PATH_ROWS),           # C3: 257 vs 497
+    ((1, 1024, 32768, 4096, BF16, BF16), T256[BF16], _lib.PATH_SPLIT),  # C4: 296 vs 352
+]
+
+
+@pytest.mark.parametrize("shape,tiles,path", MEASURED_BEST)
+def test_model_picks_the_measured_fastest_variant(shape, tiles, path):
+    pl = _lib.plan(*shape, _lib.PATH_AUTO)
+    assert (pl["tiles"], pl["path"]) == (tiles, path)
+
+
+def test_auto_is_the_first_of_the_ranking(L):
+    """AUTO and an explicit path both take the variant with the lowest
+    estimate among those that can run it; an explicit variant keeps its tiles."""
+    shape = (1, 1152, 32768, 4096, BF16, BF16)
+    best = _lib.plan(*shape, _lib.PATH_AUTO)
+    ests = []
+    for name, tiles, mask in _lib.variants(BF16):
+        for p in (_lib.PATH_EXCHANGE, _lib.PATH_SPLIT, _lib.PATH_ROWS):
+            if mask & (1 << p):
+                try:
+                    ests.append((_lib.plan(*shape, p, tiles)["est_us"], tiles, p))
+                except _lib.WtcError:
+                    pass
+    est, tiles, p = min(ests)
+    assert (best["tiles"], best["path"]) == (tiles, p) and abs(best["est_us"] - est) < 1e-9
+    pinned = _lib.plan(*shape, _lib.PATH_SPLIT, T128[BF16])
+    assert pinned["tiles"] == T128[BF16] and pinned["grid"] == 9 * 256
+
+
+def test_variant_path_errors(L):
+    # the 256-row variant runs no exchange path; rows needs k <= 128
+    with pytest.raises(_lib.WtcError) as ei:
+        _lib.plan(1, 512, 512, 64, F16, F16, _lib.PATH_EXCHANGE, T256[F16])
+    assert ei.value.code == _lib.WTC_ERR_UNSUPPORTED and "does not run the exchange" in str(ei.value)
+    with pytest.raises(_lib.WtcError) as ei:
+        _lib.plan(1, 512, 512, 256, F16, F16, _lib.PATH_ROWS, ROWS)
+    assert "k <= 128" in str(ei.value)
+    # 16-bit tiles are no variant for fp8 (its k-tile holds 128 elements); the
+    # unfused path has no rows variant
+    with pytest.raises(_lib.WtcError) as ei:
+        _lib.plan(1, 512, 512, 128, FP8, F16, _lib.PATH_AUTO, T128[F16])
+    assert "no gfx950 kernel variant" in str(ei.value) and "256x128x128/2x32" in str(ei.value)
+    with pytest.raises(_lib.WtcError):
+        _lib.plan(1, 512, 512, 64, F16, F16, _lib.PATH_UNFUSED, ROWS)
+    # an explicit variant with AUTO runs its own best path
+    assert _lib.plan(1, 512, 512, 64, F16, F16, _lib.PATH_AUTO, T256[F16])["path"] == _lib.PATH_SPLIT
+    assert _lib.plan(1, 512, 512, 64, F16, F16, _lib.PATH_AUTO, ROWS)["path"] == _lib.PATH_ROWS
 
 
 @pytest.mark.parametrize("args,code", [
@@ -151,9 +232,9 @@ def compile_chain(L, path: Path, out: Path, tiles, fused=1, errsize=4096):
     return rc, err.value
 
 
-EXPECT = {  # config -> (tile_k, path chosen for the fused kernel)
-    "C1": (32, "exchange"), "C2": (64, "exchange"), "C3": (64, "rows"),
-    "C4": (64, "split"), "C5": (128, "split"),
+EXPECT = {  # config -> (tiles of the variant the solver ranks first, its path)
+    "C1": ([128, 128, 32, 2, 32], "exchange"), "C2": (KS2[F16], "exchange"), "C3": (ROWS, "rows"),
+    "C4": (T256[BF16], "split"), "C5": (KS2[FP8], "split"),
 }
 
 
@@ -164,8 +245,8 @@ def test_solver_and_compile_per_config(L, tmp_path, name, named):
     src = write_chain(tmp_path, cfg, named_softmax=named)
     rc, tiles, err = solve(L, src, tmp_path)
     assert rc == 0, err
-    tile_k, path = EXPECT[name]
-    assert tiles == [128, 128, tile_k, 2, 32 if cfg.in_dtype == "f32" else 16]
+    want, path = EXPECT[name]
+    assert tiles == want
     summary = json.loads((tmp_path / "best_summary.json").read_text())
     assert {k: summary["problem"][k] for k in "mnk"} == {"m": cfg.m, "n": cfg.n, "k": cfg.k}
     assert {"smemBytes", "numSM", "warpSize", "elementBytes"} <= set(summary["arch"])
@@ -187,7 +268,9 @@ def test_solver_and_compile_per_config(L, tmp_path, name, named):
     assert rc == 0, err
     launch = json.loads((out / "05.out.hip.launch.json").read_text())
     assert launch["problem"]["m"] == cfg.m and launch["problem"]["n"] == cfg.n
-    assert launch["path"] == path and launch["entry"] == "wtc_matmul_softmax"
+    assert launch["path"] == path and launch["entry"] == "wtc_matmul_softmax_tiles"
+    assert [launch["tiles"][k] for k in ("tileM", "tileN", "tileK", "threadTileM",
+                                         "threadTileN")] == tiles
     assert launch["runtime_scales"] == (cfg.in_dtype == "fp8")
     assert abs(launch["logit_scale"] - cfg.logit_scale) < 1e-6
     plan_json = json.loads((out / "04.kernel.plan.json").read_text())

@@ -112,25 +112,21 @@ def test_exchange_single_column_tile(native_lib, in_dtype, out_dtype, n):
 @pytest.mark.parametrize("in_dtype,out_dtype", [("f16", "f16"), ("bf16", "f32"), ("fp8", "f16"),
                                                 ("bf16", "bf16")])
 def test_split_256_row_tiles_ragged(native_lib, in_dtype, out_dtype):
-    """The split path's 256-row tiles (chosen for an even number of 128-row
-    blocks and >= 2 tiles per CU): batch 64 x 200 rows (56 padding rows in
-    each tile), ragged N and K."""
+    """The split path's 256-row tile variant: batch 64 x 200 rows (56 padding
+    rows in each tile), ragged N and K."""
     from welder_typical_chain_amd import _lib
-    import ctypes
     batch, m, n = 64, 200, 1000
     k = {"f16": 72, "bf16": 72, "fp8": 80}[in_dtype]
-    grid = ctypes.c_int64()
-    chosen = ctypes.c_int()
-    cu = torch.cuda.get_device_properties(0).multi_processor_count
     codes = {"f16": 1, "bf16": 2, "fp8": 3, "f32": 0}
-    assert _lib.lib().wtc_plan(batch, m, n, k, codes[in_dtype], codes[out_dtype], _lib.PATH_SPLIT,
-                               cu, 1, ctypes.byref(grid), ctypes.byref(chosen), None) == 0
-    assert grid.value == batch * 1 * 8, "expected one 256-row tile per batch and column tile"
+    tiles = [256, 128, 128 // (2 if in_dtype != "fp8" else 1), 2, 32]
+    cu = torch.cuda.get_device_properties(0).multi_processor_count
+    pl = _lib.plan(batch, m, n, k, codes[in_dtype], codes[out_dtype], _lib.PATH_SPLIT, tiles, cu)
+    assert pl["grid"] == batch * 1 * 8, "expected one 256-row tile per batch and column tile"
     cfg = ChainConfig("split256", batch, m, n, k, in_dtype, out_dtype, "normal", 0.4,
                       logit_scale=0.7)
     _announce(f"split 256-row tiles {in_dtype}->{out_dtype} {batch}x{m}x{n}x{k}")
     inp = O.make_inputs(cfg, seed=11)
-    out = run_chain(inp, in_dtype, out_dtype, path="split", batched=True)
+    out = run_chain(inp, in_dtype, out_dtype, path="split", batched=True, tiles=tiles)
     _check(cfg, inp, out, np.arange(m), batches=(0, 31, 63), path="split")
 
 

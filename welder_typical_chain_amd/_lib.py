@@ -35,6 +35,18 @@ PATHS = {"auto": PATH_AUTO, "exchange": PATH_EXCHANGE, "split": PATH_SPLIT,
 _c_i64 = ctypes.c_int64
 _c_p = ctypes.c_void_p
 
+
+class Tiles(ctypes.Structure):
+    """wtc_tiles: the five best.json tile parameters of a kernel variant."""
+    _fields_ = [("tile_m", _c_i64), ("tile_n", _c_i64), ("tile_k", _c_i64),
+                ("thread_tile_m", _c_i64), ("thread_tile_n", _c_i64)]
+
+    def as_list(self):
+        return [self.tile_m, self.tile_n, self.tile_k, self.thread_tile_m, self.thread_tile_n]
+
+
+_c_tiles = ctypes.POINTER(Tiles)
+
 # name -> (restype, argtypes); every symbol the headers under include/wtc declare.
 SIGNATURES = {
     "wtc_matmul_softmax": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64,
@@ -44,6 +56,16 @@ SIGNATURES = {
     "wtc_matmul_softmax_noalloc": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64,
                                                   ctypes.c_int, ctypes.c_int, ctypes.c_float,
                                                   ctypes.c_float, ctypes.c_float, ctypes.c_int, _c_p]),
+    "wtc_matmul_softmax_tiles": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64,
+                                                ctypes.c_int, ctypes.c_int, ctypes.c_float,
+                                                ctypes.c_float, ctypes.c_float, _c_tiles,
+                                                ctypes.c_int, _c_p, ctypes.c_size_t, _c_p]),
+    "wtc_list_variants": (ctypes.c_int, [ctypes.c_int, _c_tiles, ctypes.POINTER(ctypes.c_uint),
+                                         ctypes.POINTER(ctypes.c_char_p), ctypes.c_int]),
+    "wtc_plan_tiles": (ctypes.c_int, [_c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_int, ctypes.c_int,
+                                      ctypes.c_int, _c_tiles, ctypes.c_int, ctypes.c_int, _c_tiles,
+                                      ctypes.POINTER(ctypes.c_int), ctypes.POINTER(_c_i64),
+                                      ctypes.POINTER(_c_i64), ctypes.POINTER(ctypes.c_double)]),
     "wtc_matmul_softmax_workspace_size": (_c_i64, [_c_i64, _c_i64, _c_i64, _c_i64,
                                                    ctypes.c_int, ctypes.c_int, ctypes.c_int]),
     "wtc_workspace_init": (ctypes.c_int, [_c_p, ctypes.c_size_t, _c_p]),
@@ -107,3 +129,36 @@ def lib() -> ctypes.CDLL:
 def check(code: int) -> None:
     if code != WTC_OK:
         raise WtcError(code, lib().wtc_last_error().decode())
+
+
+def variants(in_dtype: int):
+    """[(name, [tileM, tileN, tileK, threadTileM, threadTileN], paths bitmask)]
+    of the kernel variants built for an input type (wtc_list_variants)."""
+    L = lib()
+    count = L.wtc_list_variants(in_dtype, None, None, None, 0)
+    if count < 0:
+        check(WTC_ERR_ARG)
+    tiles = (Tiles * count)()
+    paths = (ctypes.c_uint * count)()
+    names = (ctypes.c_char_p * count)()
+    L.wtc_list_variants(in_dtype, tiles, paths, names, count)
+    return [(names[i].decode(), tiles[i].as_list(), int(paths[i])) for i in range(count)]
+
+
+def plan(batch: int, m: int, n: int, k: int, in_dtype: int, out_dtype: int, path: int = PATH_AUTO,
+         tiles=None, cu_count: int = 256, wg_per_cu: int = 1) -> dict:
+    """wtc_plan_tiles: the variant and path the cost model picks, with its
+    grid, workspace bytes and estimated microseconds per call."""
+    chosen = Tiles()
+    cpath = ctypes.c_int()
+    grid = ctypes.c_int64()
+    ws = ctypes.c_int64()
+    est = ctypes.c_double()
+    want = Tiles(*tiles) if tiles is not None else None
+    rc = lib().wtc_plan_tiles(batch, m, n, k, in_dtype, out_dtype, path,
+                              ctypes.byref(want) if want is not None else None, cu_count, wg_per_cu,
+                              ctypes.byref(chosen), ctypes.byref(cpath), ctypes.byref(grid),
+                              ctypes.byref(ws), ctypes.byref(est))
+    check(rc)
+    return {"tiles": chosen.as_list(), "path": cpath.value, "grid": grid.value,
+            "workspace_bytes": ws.value, "est_us": est.value}

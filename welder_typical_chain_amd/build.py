@@ -44,7 +44,7 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
 HIP_SOURCES = ["fused_matmul_softmax.hip", "rowblock_softmax.hip", "unfused_chain.hip", "launch.hip"]
-CXX_SOURCES = ["chain_recognizer.cpp", "tile_solver.cpp", "compile_capi.cpp"]
+CXX_SOURCES = ["chain_recognizer.cpp", "variants.cpp", "tile_solver.cpp", "compile_capi.cpp"]
 
 HIP_FLAGS = [
     f"--offload-arch={ARCH}",
@@ -158,7 +158,7 @@ def build(verbose: bool = False) -> Path:
     if COMPILE_LIB.is_symlink() or COMPILE_LIB.exists():
         COMPILE_LIB.unlink()
     COMPILE_LIB.symlink_to(LIB.name)
-    cpu_objs = [str(OBJ / (s + ".o")) for s in ("chain_recognizer.cpp", "tile_solver.cpp")]
+    cpu_objs = [str(OBJ / (s + ".o")) for s in ("chain_recognizer.cpp", "variants.cpp", "tile_solver.cpp")]
     tmp = SOLVER_LIB.with_suffix(".so.tmp")
     _run(["g++", "-shared", "-Wl,--no-undefined", "-o", str(tmp), *cpu_objs])
     os.replace(tmp, SOLVER_LIB)

@@ -51,12 +51,16 @@ def new_workspace(nbytes: int, device: torch.device | str = "cuda") -> torch.Ten
 def matmul_softmax(a: torch.Tensor, b: torch.Tensor, *, out: torch.Tensor | None = None,
                    out_dtype: torch.dtype | None = None, logit_scale: float = 1.0,
                    scale_a: float = 1.0, scale_b: float = 1.0, path: str = "auto",
-                   workspace: torch.Tensor | None = None, check: bool = False) -> torch.Tensor:
+                   workspace: torch.Tensor | None = None, check: bool = False,
+                   tiles=None) -> torch.Tensor:
     """out = softmax_row(logit_scale * scale_a * scale_b * (a @ b)).
 
     a: [M, K] or [batch, M, K]; b: [K, N] or [batch, K, N]; contiguous CUDA
     tensors of float32 / float16 / bfloat16 / float8_e4m3fn (or uint8 holding
-    e4m3 bytes).  Runs on the current stream of a's device.  With check=True
+    e4m3 bytes).  Runs on the current stream of a's device.  `tiles`: the five
+    best.json tile parameters of the kernel variant to run
+    (wtc_matmul_softmax_tiles; None = the variant the cost model picks).
+    With check=True
     the stream is synchronised afterwards and a timed-out exchange wait
     raises WtcError (code WTC_ERR_TIMEOUT) instead of being reported by the
     next call.
@@ -89,14 +93,20 @@ def matmul_softmax(a: torch.Tensor, b: torch.Tensor, *, out: torch.Tensor | None
     if workspace is not None:
         ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
     stream = torch.cuda.current_stream(a.device).cuda_stream
-    call = (a.data_ptr(), b.data_ptr(), out.data_ptr(), batch, m, n, k, in_code, out_code,
-            float(logit_scale), float(scale_a), float(scale_b), _lib.PATHS[path], ws_ptr,
-            ws_bytes, stream)
+    head = (a.data_ptr(), b.data_ptr(), out.data_ptr(), batch, m, n, k, in_code, out_code,
+            float(logit_scale), float(scale_a), float(scale_b))
+    tail = (_lib.PATHS[path], ws_ptr, ws_bytes, stream)
+    if tiles is None:
+        fn, call = _lib.lib().wtc_matmul_softmax, head + tail
+    else:
+        import ctypes
+        t = _lib.Tiles(*[int(x) for x in tiles])
+        fn, call = _lib.lib().wtc_matmul_softmax_tiles, head + (ctypes.byref(t),) + tail
     if a.device.index == torch.cuda.current_device():
-        rc = _lib.lib().wtc_matmul_softmax(*call)
+        rc = fn(*call)
     else:  # the library launches on the current device
         with torch.cuda.device(a.device):
-            rc = _lib.lib().wtc_matmul_softmax(*call)
+            rc = fn(*call)
     if rc:
         _lib.check(rc)
     if check:

@@ -52,35 +52,28 @@ struct TileParams {
   int64_t tile_m = 0, tile_n = 0, tile_k = 0, thread_tile_m = 0, thread_tile_n = 0;
 };
 
-// One kernel variant of the HIP library, in the reference's tile vocabulary:
-// tile_k counts elements of the input type (128 bytes of K), the thread tile
-// is the accumulator footprint of one lane (rows x columns).
-struct Variant {
-  TileParams tiles;
-  const char* name;
-};
-std::vector<Variant> supported_variants(Elem in);
-bool is_supported(const TileParams& t, Elem in);
-
 // best.json read/write with the reference's keys and regex reader
 // (compiler/scheduler/Search.cpp:12-20,35-86).
 bool load_best_json(const std::string& path, TileParams& t, std::string& diag);
 bool write_best_json(const TileParams& t, const std::string& path, std::string& diag);
 
 // ---- solver ---------------------------------------------------------------
+// One kernel variant (variants.h) with the fused path the cost model ranks
+// first for it on this problem.
 struct Candidate {
   TileParams tiles;
-  double score = 0;              // higher is better
-  double estimated_latency = 0;  // microseconds
+  std::string variant;           // variant name
+  double score = 0;              // higher is better: estimated TFLOP/s
+  double estimated_latency = 0;  // microseconds per call
   double profiled_ms = -1;
   int64_t bytes_a = 0, bytes_b = 0, bytes_c = 0, bytes_cut = 0;
-  std::string path;              // exchange | split
+  std::string path;              // exchange | split | rows
 };
 struct ArchInfo {
   int64_t lds_bytes = 160 * 1024;
   int64_t num_cu = 256;
   int64_t wave_size = 64;
-  double clock_ghz = 2.4;
+  double clock_ghz = 2.4;  // peak engine clock (the cost model uses the clock under load)
   double hbm_gbs = 8000.0;
 };
 std::vector<Candidate> solve(const ChainSpec& spec, int64_t max_connect_level,

@@ -15,21 +15,21 @@
 #include <vector>
 
 #include "chain_spec.h"
+#include "variants.h"
 #include "wtc/welder_compile_capi.h"
 #include "wtc/wtc_hip.h"
 
 namespace wtc {
 
-// Workgroup sizes of the kernels and the split path's tile height (defined
-// with the kernels and the launcher in the library).
+// Workgroup sizes of the kernels (defined with the kernels and the launcher
+// in the library).
 int chain_kernel_threads(int in_dt);
 int rows_kernel_threads();
-int split_tile_rows(int in_dt, int64_t batch, int64_t m, int64_t n, int cu_count);
 int rescale_waves_per_row(int64_t rows_total, int cu_count);
 // Compute units of the current device, or `fallback` when no GPU is visible.
 int device_cu_count(int fallback);
-// Dynamic LDS bytes the launcher adds to the exchange kernel.
-int exchange_lds_pad(int in_dt, int out_dt);
+// Dynamic LDS bytes the launcher adds to the exchange kernel of wave layout ks.
+int exchange_lds_pad(int in_dt, int out_dt, int ks);
 
 static std::string library_path() {
   Dl_info info{};
@@ -126,26 +126,43 @@ static int compile_impl(const char* input_mlir_path, const char* out_dir, int64_
     return session_fail(std::string("cannot read input MLIR: ") + input_mlir_path);
   ChainSpec spec;
   if (!recognize_chain(text, spec, diag)) return session_fail("chain not recognised: " + diag);
-  const TileParams tiles{tile_m, tile_n, tile_k, thread_tile_m, thread_tile_n};
-  if (!is_supported(tiles, spec.in)) {
+  const int in_code = elem_to_dtype_code(spec.in), out_code = elem_to_dtype_code(spec.out);
+  VariantDesc var{};
+  if (!find_variant(in_code, tile_m, tile_n, tile_k, thread_tile_m, thread_tile_n, &var)) {
     std::ostringstream o;
     o << "no gfx950 kernel variant implements tile " << tile_m << "x" << tile_n << "x" << tile_k
       << " thread tile " << thread_tile_m << "x" << thread_tile_n << " for "
       << elem_mlir_name(spec.in) << "; available:";
-    for (const Variant& v : supported_variants(spec.in))
-      o << " " << v.tiles.tile_m << "x" << v.tiles.tile_n << "x" << v.tiles.tile_k << "/"
-        << v.tiles.thread_tile_m << "x" << v.tiles.thread_tile_n;
+    for (const VariantDesc& v : variants_for(in_code))
+      o << " " << v.tile_m << "x" << v.tile_n << "x" << v.tile_k << "/" << v.thread_tile_m << "x"
+        << v.thread_tile_n << " (" << v.name << ")";
     return session_fail(o.str());
   }
-  const int in_code = elem_to_dtype_code(spec.in), out_code = elem_to_dtype_code(spec.out);
   // Plan for the current device (MI355X's 256 CUs without one); the
-  // exchange kernel's LDS footprint holds one of its workgroups per CU.
+  // exchange kernel's LDS footprint holds one of its workgroups per CU.  The
+  // fused chain runs the variant of the given tiles on the path the cost
+  // model ranks first for it.  The unfused baseline runs the same variant
+  // when it has a logits epilogue; the rows variant has none (it only runs
+  // fused), and then the baseline takes the variant ranked first for the
+  // unfused path.
   const int cu_count = device_cu_count(256);
   const int path_req = fused ? WTC_PATH_AUTO : WTC_PATH_UNFUSED;
+  const VariantDesc requested = var;
+  wtc_tiles want{tile_m, tile_n, tile_k, thread_tile_m, thread_tile_n};
+  if (!fused && !(var.paths & (1u << WTC_PATH_UNFUSED))) {
+    wtc_tiles best{};
+    if (wtc_plan_tiles(spec.batch, spec.m, spec.n, spec.k, in_code, out_code, WTC_PATH_UNFUSED,
+                       nullptr, cu_count, 1, &best, nullptr, nullptr, nullptr, nullptr) != WTC_OK)
+      return session_fail(std::string("launch plan failed: ") + wtc_last_error());
+    want = best;
+    find_variant(in_code, want.tile_m, want.tile_n, want.tile_k, want.thread_tile_m,
+                 want.thread_tile_n, &var);
+  }
   int64_t grid = 0, ws = 0;
   int path = 0;
-  if (wtc_plan(spec.batch, spec.m, spec.n, spec.k, in_code, out_code, path_req, cu_count, 1, &grid,
-               &path, &ws) != WTC_OK)
+  double est_us = 0;
+  if (wtc_plan_tiles(spec.batch, spec.m, spec.n, spec.k, in_code, out_code, path_req, &want,
+                     cu_count, 1, nullptr, &path, &grid, &ws, &est_us) != WTC_OK)
     return session_fail(std::string("launch plan failed: ") + wtc_last_error());
 
   std::error_code ec;
@@ -172,24 +189,24 @@ static int compile_impl(const char* input_mlir_path, const char* out_dir, int64_
   std::vector<K> ks;
   const int64_t rows = spec.batch * spec.m;
   const int tile_threads = chain_kernel_threads(in_code);
+  const std::string layout = std::to_string(var.tile_rows) + "x128" + (var.ks == 2 ? ",ksplit2" : "");
   if (path == WTC_PATH_ROWS) {
     ks.push_back({"chain_rows_kernel<" + kin + "," + kout + ">",
                   "_ZN3wtc17chain_rows_kernelILi" + std::to_string(in_code) + "ELi" +
                       std::to_string(out_code) + "E",
                   grid, 0, rows_kernel_threads()});
   } else if (path == WTC_PATH_EXCHANGE) {
-    ks.push_back({"chain_tile_kernel<" + kin + "," + kout + ",exchange>",
-                  chain_sym(in_code, out_code, 0, 128, in_code == 0 ? 1 : 2), grid,
-                  exchange_lds_pad(in_code, out_code), tile_threads});
+    ks.push_back({"chain_tile_kernel<" + kin + "," + kout + ",exchange," + layout + ">",
+                  chain_sym(in_code, out_code, 0, 128, var.ks), grid,
+                  exchange_lds_pad(in_code, out_code, var.ks), tile_threads});
   } else if (path == WTC_PATH_SPLIT) {
-    const int tm = split_tile_rows(in_code, spec.batch, spec.m, spec.n, cu_count);
-    ks.push_back({"chain_tile_kernel<" + kin + "," + kout + ",split," + std::to_string(tm) + "x128>",
-                  chain_sym(in_code, out_code, 1, tm), grid, 0, tile_threads});
+    ks.push_back({"chain_tile_kernel<" + kin + "," + kout + ",split," + layout + ">",
+                  chain_sym(in_code, out_code, 1, var.tile_rows, var.ks), grid, 0, tile_threads});
     ks.push_back({"rescale_rows_kernel<" + kout + ">", "_ZN3wtc19rescale_rows_kernel" + out_t,
                   (rows * rescale_waves_per_row(rows, cu_count) + 3) / 4, 0});
   } else {
-    ks.push_back({"chain_tile_kernel<" + kin + ",f32,logits>", chain_sym(in_code, 0, 2), grid, 0,
-                  tile_threads});
+    ks.push_back({"chain_tile_kernel<" + kin + ",f32,logits," + layout + ">",
+                  chain_sym(in_code, 0, 2, var.tile_rows, var.ks), grid, 0, tile_threads});
     ks.push_back({"rowmax_kernel", "_ZN3wtc13rowmax_kernel", rows, 0});
     ks.push_back({"expsub_kernel", "_ZN3wtc13expsub_kernel", rows, 0});
     ks.push_back({"rowsum_kernel", "_ZN3wtc13rowsum_kernel", rows, 0});
@@ -197,11 +214,17 @@ static int compile_impl(const char* input_mlir_path, const char* out_dir, int64_
   }
 
   std::ostringstream plan;
-  plan << "{\n  \"target\": \"gfx950\",\n  \"variant\": \"" << supported_variants(spec.in).front().name
-       << "\",\n  \"path\": \"" << path_name(path) << "\",\n  \"fused\": " << (fused ? "true" : "false")
-       << ",\n  \"max_connect_level\": " << max_connect_level << ",\n  \"tiles\": {\"tileM\": " << tile_m
-       << ", \"tileN\": " << tile_n << ", \"tileK\": " << tile_k << ", \"threadTileM\": " << thread_tile_m
-       << ", \"threadTileN\": " << thread_tile_n << "},\n  \"kernels\": [\n";
+  auto tiles_json = [](const wtc_tiles& t) {
+    return "{\"tileM\": " + std::to_string(t.tile_m) + ", \"tileN\": " + std::to_string(t.tile_n) +
+           ", \"tileK\": " + std::to_string(t.tile_k) + ", \"threadTileM\": " +
+           std::to_string(t.thread_tile_m) + ", \"threadTileN\": " + std::to_string(t.thread_tile_n) + "}";
+  };
+  const wtc_tiles asked{tile_m, tile_n, tile_k, thread_tile_m, thread_tile_n};
+  plan << "{\n  \"target\": \"gfx950\",\n  \"variant\": \"" << var.name << "\",\n  \"requested_variant\": \""
+       << requested.name << "\",\n  \"path\": \"" << path_name(path) << "\",\n  \"fused\": "
+       << (fused ? "true" : "false") << ",\n  \"max_connect_level\": " << max_connect_level
+       << ",\n  \"tiles\": " << tiles_json(want) << ",\n  \"requested_tiles\": " << tiles_json(asked)
+       << ",\n  \"estimated_us\": " << est_us << ",\n  \"kernels\": [\n";
   for (size_t i = 0; i < ks.size(); ++i)
     plan << "    {\"name\": \"" << ks[i].name << "\", \"grid\": [" << ks[i].grid
          << ", 1, 1], \"block\": [" << ks[i].block << ", 1, 1], \"dynamic_lds_bytes\": " << ks[i].lds
@@ -211,7 +234,8 @@ static int compile_impl(const char* input_mlir_path, const char* out_dir, int64_
 
   std::ostringstream launch;
   launch << "{\n  \"format\": \"wtc-hip-launch-v1\",\n  \"target\": \"gfx950\",\n  \"library\": \"" << lib
-         << "\",\n  \"entry\": \"wtc_matmul_softmax\",\n  \"problem\": {\"batch\": " << spec.batch
+         << "\",\n  \"entry\": \"wtc_matmul_softmax_tiles\",\n  \"variant\": \"" << var.name
+         << "\",\n  \"tiles\": " << tiles_json(want) << ",\n  \"problem\": {\"batch\": " << spec.batch
          << ", \"m\": " << spec.m << ", \"n\": " << spec.n << ", \"k\": " << spec.k
          << ", \"batched\": " << (spec.batched ? "true" : "false") << "},\n  \"in_dtype\": \"" << kin
          << "\",\n  \"out_dtype\": \"" << kout << "\",\n  \"chain_acc_dtype\": \"" << elem_mlir_name(spec.acc)
@@ -281,7 +305,8 @@ static int compile_impl(const char* input_mlir_path, const char* out_dir, int64_
   wg << "// Launch plan of the fused Matmul -> row-Softmax chain on gfx950: one\n"
      << "// launch operation per HIP kernel of the " << path_name(path) << " path.  The kernel\n"
      << "// bodies are in the code object 05.out.gfx950.hsaco (library " << lib << "),\n"
-     << "// launched by wtc_matmul_softmax; the workspace holds the row statistics.\n"
+     << "// launched by wtc_matmul_softmax_tiles (variant " << var.name << "); the workspace\n"
+     << "// holds the row statistics.\n"
      << "module attributes {gpu.container_module, wtc.target = \"gfx950\", wtc.path = \""
      << path_name(path) << "\", wtc.compute_units = " << cu_count << " : i32} {\n"
      << "  gpu.module @wtc_kernels [#rocdl.target<chip = \"gfx950\">] {\n  }\n"
@@ -302,10 +327,12 @@ static int compile_impl(const char* input_mlir_path, const char* out_dir, int64_
   wg << "    return\n  }\n}\n";
   std::ostringstream run;
   run << "// Runnable artefact of the chain for gfx950 (no NVVM is involved): the HIP\n"
-      << "// code object 05.out.gfx950.hsaco, run through wtc_matmul_softmax with the\n"
+      << "// code object 05.out.gfx950.hsaco, run through wtc_matmul_softmax_tiles with the\n"
       << "// arguments below.  Per-kernel resources are in kernel_report.txt.\n"
       << "module attributes {wtc.target = \"gfx950\", wtc.code_object = \"05.out.gfx950.hsaco\", "
-      << "wtc.library = \"" << lib << "\", wtc.entry = \"wtc_matmul_softmax\", wtc.path = \""
+      << "wtc.library = \"" << lib << "\", wtc.entry = \"wtc_matmul_softmax_tiles\", wtc.variant = \""
+      << var.name << "\", wtc.tiles = [" << want.tile_m << ", " << want.tile_n << ", " << want.tile_k
+      << ", " << want.thread_tile_m << ", " << want.thread_tile_n << "], wtc.path = \""
       << path_name(path) << "\", wtc.path_code = " << path << " : i32, wtc.in_dtype = " << in_code
       << " : i32, wtc.out_dtype = " << out_code << " : i32, wtc.batch = " << spec.batch
       << " : i64, wtc.m = " << spec.m << " : i64, wtc.n = " << spec.n << " : i64, wtc.k = " << spec.k

@@ -1236,12 +1236,30 @@ static const void* split256_by_in(int in_dt, int out_dt) {
   return nullptr;
 }
 
+// f32 logits (the unfused path's first kernel) on the 256-row and k-split
+// layouts, so that every tile variant also runs the unfused chain.
+template <int TM, int KS>
+static const void* logits_by_in(int in_dt) {
+  switch (in_dt) {
+    case DT_F16: return tile_kernel_ptr<DT_F16, DT_F32, kEpiLogits, TM, KS>();
+    case DT_BF16: return tile_kernel_ptr<DT_BF16, DT_F32, kEpiLogits, TM, KS>();
+    case DT_FP8: return tile_kernel_ptr<DT_FP8, DT_F32, kEpiLogits, TM, KS>();
+  }
+  return nullptr;
+}
+
 const void* chain_kernel_symbol(int in_dt, int out_dt, int epi, int tile_rows, int ks) {
-  if (tile_rows == 256) return epi == kEpiSplit && ks == 1 ? split256_by_in(in_dt, out_dt) : nullptr;
+  if (tile_rows == 256) {
+    if (ks != 1) return nullptr;
+    if (epi == kEpiSplit) return split256_by_in(in_dt, out_dt);
+    if (epi == kEpiLogits) return out_dt == DT_F32 ? logits_by_in<256, 1>(in_dt) : nullptr;
+    return nullptr;
+  }
   if (tile_rows != 128) return nullptr;
   if (ks == 2) {
     if (epi == kEpiExchange) return ksplit_by_in<kEpiExchange>(in_dt, out_dt);
     if (epi == kEpiSplit) return ksplit_by_in<kEpiSplit>(in_dt, out_dt);
+    if (epi == kEpiLogits) return out_dt == DT_F32 ? logits_by_in<128, 2>(in_dt) : nullptr;
     return nullptr;
   }
   if (ks != 1) return nullptr;

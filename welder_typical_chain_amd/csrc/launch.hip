@@ -15,6 +15,7 @@
 #include <vector>
 
 #include "tile_layout.h"
+#include "variants.h"
 #include "wtc/wtc_hip.h"
 #include "wtc_kernels.h"
 
@@ -27,17 +28,6 @@ int rescale_waves_per_row(int64_t rows_total, int cu_count) {
   return wpr;
 }
 
-// Tile height of the split path: 256-row tiles (a quarter less L2 and a
-// third less LDS traffic per MFMA) for 16-bit and fp8 inputs when they add
-// no padding rows (an even number of 128-row blocks) and the problem still
-// gives every CU at least two of them; 128 otherwise.
-int split_tile_rows(int in_dt, int64_t batch, int64_t m, int64_t n, int cu_count) {
-  if (in_dt == DT_F32) return 128;
-  const int64_t rb128 = (m + 127) / 128;
-  const int64_t tiles256 = batch * (rb128 / 2) * ((n + 127) / 128);
-  return rb128 % 2 == 0 && tiles256 >= 2 * (int64_t)cu_count ? 256 : 128;
-}
-
 // Compute units of the current device, or `fallback` when no GPU is visible
 // (the compile C-ABI also runs on build hosts).
 int device_cu_count(int fallback) {
@@ -48,27 +38,24 @@ int device_cu_count(int fallback) {
   return prop.multiProcessorCount;
 }
 
-// Wave layout of the exchange path's 128-row tiles: k-split (ks = 2) for
-// 16-bit and fp8 inputs, 4 waves of 64x64 for f32.
-int exchange_ks(int in_dt) { return in_dt == DT_F32 ? 1 : 2; }
-
-// Dynamic LDS added to the exchange kernel so that no CU holds two of its
-// workgroups (spreads a grid of <= CU-count tiles over all CUs).
-int exchange_lds_pad(int in_dt, int out_dt) {
-  const int stat = chain_kernel_lds_bytes(in_dt, out_dt, exchange_ks(in_dt));
+// Dynamic LDS added to an exchange kernel (wave layout `ks`) so that no CU
+// holds two of its workgroups (spreads a grid of <= CU-count tiles over all
+// CUs).
+int exchange_lds_pad(int in_dt, int out_dt, int ks) {
+  const int stat = chain_kernel_lds_bytes(in_dt, out_dt, ks);
   const int want = 80 * 1024 + 1024;
   return stat >= want ? 0 : want - stat;
 }
+
+static_assert(kExchangeMaxTiles == kMaxExchangeTiles, "exchange slot limit");
 }  // namespace wtc
 
 namespace {
 
 using namespace wtc;
 
-constexpr int kTile = 128;            // BM = BN of chain_tile_kernel
+constexpr int kTile = 128;            // BN of chain_tile_kernel, rows of the exchange tiles
 constexpr int kRescaleRowsPerWg = 4;  // rescale_rows_kernel
-constexpr int kRescaleMaxTiles = 512;
-constexpr int kExchangeMaxColTiles = 64;  // one lane per column tile of a row block
 constexpr uint64_t kDefaultSpinTicks = 200000000ull;  // 2 s of the 100 MHz clock
 constexpr int kMaxDevices = 64;
 constexpr int64_t kMinDefaultWorkspace = 1 << 20;
@@ -143,47 +130,63 @@ int check_args(int64_t batch, int64_t m, int64_t n, int64_t k, int in_dt, int ou
   return WTC_OK;
 }
 
-int plan_impl(int64_t batch, int64_t m, int64_t n, int64_t k, int in_dt, int out_dt,
-              int path, int cu_count, int wg_per_cu, int64_t* grid, int* chosen,
-              int64_t* ws_bytes) {
+struct Plan {
+  VariantDesc v{};
+  int path = 0;
+  int64_t grid = 0, ws = 0;
+  double est_us = 0;
+};
+
+std::string tiles_text(const wtc_tiles& t) {
+  return std::to_string(t.tile_m) + "x" + std::to_string(t.tile_n) + "x" + std::to_string(t.tile_k) +
+         "/" + std::to_string(t.thread_tile_m) + "x" + std::to_string(t.thread_tile_n);
+}
+
+// The variant and path to run: the cost model's first choice among the
+// variants allowed (`tiles`, or all) and the paths allowed (`path`; AUTO =
+// the fused ones).  `xch_per_cu`: exchange-kernel workgroups one CU holds.
+int plan_impl(int64_t batch, int64_t m, int64_t n, int64_t k, int in_dt, int out_dt, int path,
+              const wtc_tiles* tiles, int cu_count, int xch_per_cu, Plan* out) {
   int rc = check_args(batch, m, n, k, in_dt, out_dt, path);
   if (rc) return rc;
-  const int64_t tiles = batch * ceil_div(m, kTile) * ceil_div(n, kTile);
-  const int64_t capacity = (int64_t)cu_count * (int64_t)wg_per_cu;
-  int p = path;
-  const int64_t nT = ceil_div(n, kTile);
-  const int64_t rbs = batch * ceil_div(m, kTile);
-  const bool fits = tiles <= capacity && nT <= kExchangeMaxColTiles && tiles <= kMaxExchangeTiles;
-  const bool rows_ok = (in_dt == DT_F16 || in_dt == DT_BF16) && k <= rows_kernel_max_k();
-  if (p == WTC_PATH_AUTO) {
-    if (rows_ok && (!fits || rbs >= (int64_t)cu_count))
-      p = WTC_PATH_ROWS;
-    else
-      p = fits ? WTC_PATH_EXCHANGE : WTC_PATH_SPLIT;
+  if (cu_count <= 0) return fail(WTC_ERR_ARG, "cu_count must be positive");
+  int vid = -1;
+  if (tiles) {
+    VariantDesc v;
+    if (!find_variant(in_dt, tiles->tile_m, tiles->tile_n, tiles->tile_k, tiles->thread_tile_m,
+                      tiles->thread_tile_n, &v)) {
+      std::string msg = "no gfx950 kernel variant has tiles " + tiles_text(*tiles) +
+                        " for this input type; available:";
+      for (const VariantDesc& d : variants_for(in_dt))
+        msg += " " + tiles_text(wtc_tiles{d.tile_m, d.tile_n, d.tile_k, d.thread_tile_m, d.thread_tile_n});
+      return fail(WTC_ERR_UNSUPPORTED, msg);
+    }
+    vid = v.id;
   }
-  if (p == WTC_PATH_ROWS && !rows_ok)
-    return fail(WTC_ERR_UNSUPPORTED, "rows path needs 16-bit inputs and k <= " +
-                                         std::to_string(rows_kernel_max_k()));
-  if (p == WTC_PATH_EXCHANGE && tiles > capacity)
-    return fail(WTC_ERR_UNSUPPORTED,
-                "exchange path needs every tile co-resident: " + std::to_string(tiles) +
-                    " tiles > " + std::to_string(capacity) + " resident workgroups");
-  if (p == WTC_PATH_EXCHANGE && (nT > kExchangeMaxColTiles || tiles > kMaxExchangeTiles))
-    return fail(WTC_ERR_UNSUPPORTED, "exchange path supports n <= 8192 and <= " +
-                                         std::to_string(kMaxExchangeTiles) + " tiles");
-  if (p == WTC_PATH_SPLIT && ceil_div(n, kTile) > kRescaleMaxTiles)
-    return fail(WTC_ERR_UNSUPPORTED, "split path supports n <= 65536");
-  if (tiles > 0x7FFFFFFFll) return fail(WTC_ERR_UNSUPPORTED, "too many tiles for one grid");
-  if (grid) {
-    if (p == WTC_PATH_ROWS)
-      *grid = rbs;
-    else if (p == WTC_PATH_SPLIT)
-      *grid = batch * ceil_div(m, split_tile_rows(in_dt, batch, m, n, cu_count)) * nT;
-    else
-      *grid = tiles;
+  const Problem pr{batch, m, n, k, in_dt, out_dt, cu_count, xch_per_cu};
+  const std::vector<Choice> cs = rank_choices(pr, path, vid);
+  if (cs.empty()) {
+    // the reason of the first variant that implements the path asked for
+    std::string why = "no kernel variant runs this problem";
+    for (const VariantDesc& d : variants_for(in_dt)) {
+      if (vid >= 0 && d.id != vid) continue;
+      const int q = path == WTC_PATH_AUTO ? WTC_PATH_SPLIT : path;
+      const std::string r = infeasible_reason(d, q, pr);
+      if (!r.empty()) {
+        why = r;
+        if (d.paths & (1u << q)) break;
+      }
+    }
+    return fail(WTC_ERR_UNSUPPORTED, why);
   }
-  if (chosen) *chosen = p;
-  if (ws_bytes) *ws_bytes = ws_layout(batch, m, n, p).total;
+  const Choice& c = cs.front();
+  const int64_t grid = variant_grid(c.v, c.path, pr);
+  if (grid > 0x7FFFFFFFll) return fail(WTC_ERR_UNSUPPORTED, "too many tiles for one grid");
+  out->v = c.v;
+  out->path = c.path;
+  out->grid = grid;
+  out->ws = ws_layout(batch, m, n, c.path).total;
+  out->est_us = c.est_us;
   return WTC_OK;
 }
 
@@ -199,7 +202,7 @@ struct StreamWorkspace {
 struct DeviceState {
   bool init = false;
   int cu_count = 0;
-  int occ[4][3] = {};  // exchange-kernel workgroups per CU, [in_dt][out_dt]
+  int occ[4][3] = {};  // exchange-kernel workgroups per CU (fewest of the layouts), [in_dt][out_dt]
   std::vector<StreamWorkspace> ws;
   std::vector<void*> retired;
   // Host-visible word the exchange kernels set when a wait times out
@@ -234,14 +237,20 @@ int device_state(int dev, DeviceState** out, bool host_objects = true) {
     hipDeviceProp_t prop;
     HIP_TRY(hipGetDeviceProperties(&prop, dev));
     s.cu_count = prop.multiProcessorCount;
+    if (rows_kernel_max_k() != kRowsMaxK)
+      return fail(WTC_ERR_HIP, "the rows kernel's k limit differs from the variant table's");
     for (int i = 0; i < 4; ++i)
       for (int o = 0; o < 3; ++o) {
-        const void* fn = chain_kernel_symbol(i, o, kEpiExchange, 128, exchange_ks(i));
-        const int pad = exchange_lds_pad(i, o);
-        HIP_TRY(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, pad));
-        int nb = 0;
-        HIP_TRY(hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, fn, chain_kernel_threads(i), pad));
-        s.occ[i][o] = nb;
+        s.occ[i][o] = 1 << 30;
+        for (int ks = 1; ks <= 2; ++ks) {
+          const void* fn = chain_kernel_symbol(i, o, kEpiExchange, 128, ks);
+          if (!fn) continue;  // f32 has no k-split layout
+          const int pad = exchange_lds_pad(i, o, ks);
+          HIP_TRY(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, pad));
+          int nb = 0;
+          HIP_TRY(hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, fn, chain_kernel_threads(i), pad));
+          if (nb < s.occ[i][o]) s.occ[i][o] = nb;
+        }
       }
     s.init = true;
   }
@@ -329,6 +338,7 @@ int launch_chain(const void* kern, int threads, int64_t grid, int lds_dyn,
 // hipEventRecord after the launch adds a gap of 1-3 us between kernels.
 int launch_tile(const void* kern, int threads, int64_t grid, int lds_dyn,
                 const ChainParams& prm, hipStream_t stream, hipEvent_t done = nullptr) {
+  if (!kern) return fail(WTC_ERR_UNSUPPORTED, "no kernel built for this variant and path");
   ChainParams p = prm;
   const uint8_t* a = p.a;
   const uint8_t* b = p.b;
@@ -401,8 +411,8 @@ int scratch_address(int dev, void** out) {
 
 int matmul_softmax_impl(const void* a, const void* b, void* out, int64_t batch, int64_t m,
                         int64_t n, int64_t k, int in_dtype, int out_dtype, float logit_scale,
-                        float scale_a, float scale_b, int path, void* workspace,
-                        size_t workspace_bytes, void* stream_, bool noalloc);
+                        float scale_a, float scale_b, const wtc_tiles* tiles, int path,
+                        void* workspace, size_t workspace_bytes, void* stream_, bool noalloc);
 
 }  // namespace
 
@@ -415,9 +425,42 @@ const char* wtc_version(void) { return "wtc-mi355x 0.2.0 (gfx950)"; }
 int wtc_plan(int64_t batch, int64_t m, int64_t n, int64_t k, int in_dtype, int out_dtype,
              int path, int cu_count, int wg_per_cu, int64_t* grid, int* chosen_path,
              int64_t* workspace_bytes) {
+  return wtc_plan_tiles(batch, m, n, k, in_dtype, out_dtype, path, nullptr, cu_count, wg_per_cu,
+                        nullptr, chosen_path, grid, workspace_bytes, nullptr);
+}
+
+int wtc_plan_tiles(int64_t batch, int64_t m, int64_t n, int64_t k, int in_dtype, int out_dtype,
+                   int path, const wtc_tiles* tiles, int cu_count, int wg_per_cu,
+                   wtc_tiles* chosen_tiles, int* chosen_path, int64_t* grid,
+                   int64_t* workspace_bytes, double* estimated_us) {
   g_last_error.clear();
-  return plan_impl(batch, m, n, k, in_dtype, out_dtype, path, cu_count, wg_per_cu, grid,
-                   chosen_path, workspace_bytes);
+  Plan pl;
+  const int rc = plan_impl(batch, m, n, k, in_dtype, out_dtype, path, tiles, cu_count, wg_per_cu, &pl);
+  if (rc) return rc;
+  if (chosen_tiles)
+    *chosen_tiles = wtc_tiles{pl.v.tile_m, pl.v.tile_n, pl.v.tile_k, pl.v.thread_tile_m, pl.v.thread_tile_n};
+  if (chosen_path) *chosen_path = pl.path;
+  if (grid) *grid = pl.grid;
+  if (workspace_bytes) *workspace_bytes = pl.ws;
+  if (estimated_us) *estimated_us = pl.est_us;
+  return WTC_OK;
+}
+
+int wtc_list_variants(int in_dtype, wtc_tiles* tiles, unsigned* paths, const char** names,
+                      int capacity) {
+  g_last_error.clear();
+  if (!valid_in(in_dtype)) {
+    fail(WTC_ERR_ARG, "unsupported in_dtype");
+    return -1;
+  }
+  const std::vector<VariantDesc> vs = variants_for(in_dtype);
+  for (int i = 0; i < (int)vs.size() && i < capacity; ++i) {
+    const VariantDesc& v = vs[i];
+    if (tiles) tiles[i] = wtc_tiles{v.tile_m, v.tile_n, v.tile_k, v.thread_tile_m, v.thread_tile_n};
+    if (paths) paths[i] = v.paths;
+    if (names) names[i] = v.name;
+  }
+  return (int)vs.size();
 }
 
 int64_t wtc_matmul_softmax_workspace_size(int64_t batch, int64_t m, int64_t n, int64_t k,
@@ -487,7 +530,16 @@ int wtc_matmul_softmax(const void* a, const void* b, void* out, int64_t batch, i
                        size_t workspace_bytes, void* stream) {
   g_last_error.clear();
   return matmul_softmax_impl(a, b, out, batch, m, n, k, in_dtype, out_dtype, logit_scale, scale_a,
-                             scale_b, path, workspace, workspace_bytes, stream, false);
+                             scale_b, nullptr, path, workspace, workspace_bytes, stream, false);
+}
+
+int wtc_matmul_softmax_tiles(const void* a, const void* b, void* out, int64_t batch, int64_t m,
+                             int64_t n, int64_t k, int in_dtype, int out_dtype, float logit_scale,
+                             float scale_a, float scale_b, const wtc_tiles* tiles, int path,
+                             void* workspace, size_t workspace_bytes, void* stream) {
+  g_last_error.clear();
+  return matmul_softmax_impl(a, b, out, batch, m, n, k, in_dtype, out_dtype, logit_scale, scale_a,
+                             scale_b, tiles, path, workspace, workspace_bytes, stream, false);
 }
 
 int wtc_matmul_softmax_noalloc(const void* a, const void* b, void* out, int64_t batch, int64_t m,
@@ -496,7 +548,7 @@ int wtc_matmul_softmax_noalloc(const void* a, const void* b, void* out, int64_t 
                                void* stream) {
   g_last_error.clear();
   return matmul_softmax_impl(a, b, out, batch, m, n, k, in_dtype, out_dtype, logit_scale, scale_a,
-                             scale_b, path, nullptr, 0, stream, true);
+                             scale_b, nullptr, path, nullptr, 0, stream, true);
 }
 
 }  // extern "C"
@@ -505,8 +557,8 @@ namespace {
 
 int matmul_softmax_impl(const void* a, const void* b, void* out, int64_t batch, int64_t m,
                         int64_t n, int64_t k, int in_dtype, int out_dtype, float logit_scale,
-                        float scale_a, float scale_b, int path, void* workspace,
-                        size_t workspace_bytes, void* stream_, bool noalloc) {
+                        float scale_a, float scale_b, const wtc_tiles* tiles, int path,
+                        void* workspace, size_t workspace_bytes, void* stream_, bool noalloc) {
   hipStream_t stream = static_cast<hipStream_t>(stream_);
   int rc = check_args(batch, m, n, k, in_dtype, out_dtype, path);
   if (rc) return rc;
@@ -527,11 +579,13 @@ int matmul_softmax_impl(const void* a, const void* b, void* out, int64_t batch, 
   rc = take_mailbox(ds);
   if (rc) return rc;
 
-  int64_t grid = 0, need = 0;
-  int chosen = 0;
-  rc = plan_impl(batch, m, n, k, in_dtype, out_dtype, path, ds->cu_count,
-                 ds->occ[in_dtype][out_dtype], &grid, &chosen, &need);
+  Plan pl;
+  rc = plan_impl(batch, m, n, k, in_dtype, out_dtype, path, tiles, ds->cu_count,
+                 ds->occ[in_dtype][out_dtype], &pl);
   if (rc) return rc;
+  const int64_t grid = pl.grid, need = pl.ws;
+  const int chosen = pl.path;
+  const VariantDesc& var = pl.v;
 
   void* ws = workspace;
   if (noalloc) {
@@ -572,9 +626,8 @@ int matmul_softmax_impl(const void* a, const void* b, void* out, int64_t batch, 
   p.ldo_bytes = n * osz;
   p.c2 = lin * 1.4426950408889634f;
   p.lin_scale = lin;
-  // row blocks per batch of the tile kernel that runs
-  const int tile_rows =
-      chosen == WTC_PATH_SPLIT ? split_tile_rows(in_dtype, batch, m, n, ds->cu_count) : kTile;
+  // row blocks per batch of the kernel that runs
+  const int tile_rows = var.tile_rows;
   p.nRB = (int)ceil_div(m, tile_rows);
   p.nT = (int)ceil_div(n, kTile);
   p.partial = reinterpret_cast<float2*>(wsb + L.stats_off);
@@ -589,12 +642,11 @@ int matmul_softmax_impl(const void* a, const void* b, void* out, int64_t batch, 
                         p, stream);
   }
   if (chosen == WTC_PATH_EXCHANGE)
-    return launch_exchange(ds,
-                           chain_kernel_symbol(in_dtype, out_dtype, kEpiExchange, 128, exchange_ks(in_dtype)),
-                           chain_kernel_threads(in_dtype), grid, exchange_lds_pad(in_dtype, out_dtype), p,
-                           stream);
+    return launch_exchange(ds, chain_kernel_symbol(in_dtype, out_dtype, kEpiExchange, 128, var.ks),
+                           chain_kernel_threads(in_dtype), grid,
+                           exchange_lds_pad(in_dtype, out_dtype, var.ks), p, stream);
   if (chosen == WTC_PATH_SPLIT) {
-    rc = launch_tile(chain_kernel_symbol(in_dtype, out_dtype, kEpiSplit, tile_rows),
+    rc = launch_tile(chain_kernel_symbol(in_dtype, out_dtype, kEpiSplit, tile_rows, var.ks),
                      chain_kernel_threads(in_dtype), grid, 0, p, stream);
     if (rc) return rc;
     uint8_t* o = p.out;
@@ -618,7 +670,7 @@ int matmul_softmax_impl(const void* a, const void* b, void* out, int64_t batch, 
   q.out = reinterpret_cast<uint8_t*>(logits);
   q.o_bstride = m * n * 4;
   q.ldo_bytes = n * 4;
-  rc = launch_tile(chain_kernel_symbol(in_dtype, DT_F32, kEpiLogits),
+  rc = launch_tile(chain_kernel_symbol(in_dtype, DT_F32, kEpiLogits, tile_rows, var.ks),
                    chain_kernel_threads(in_dtype), grid, 0, q, stream);
   if (rc) return rc;
   const int64_t rows = batch * m;

@@ -6,7 +6,8 @@
 // reference searches a large tile space with an analytic traffic model
 // (solveGeneric, solver/WelderSolverSolveEntrypoints.h:157-265) because it
 // generates code for any tile; here the kernels are hand-written, so the space
-// is the set of instantiated variants and the model is MI355X's roofline.
+// is the set of built variants and the model is a latency estimate
+// calibrated on MI355X (variants.cpp).
 #include <algorithm>
 #include <cmath>
 #include <filesystem>
@@ -15,29 +16,11 @@
 #include <sstream>
 
 #include "chain_spec.h"
+#include "variants.h"
 #include "wtc/welder_solver_capi.h"
 #include "wtc/wtc_hip.h"
 
 namespace wtc {
-
-// The kernel library's variants: a 128x128 output tile per workgroup, one
-// 128-byte k-tile per pipeline step.  16-bit and fp8 inputs run 8 waves of
-// 64x32 (each lane: 2 output rows x 16 columns of accumulators), f32 runs 4
-// waves of 64x64 (2 rows x 32 columns).
-std::vector<Variant> supported_variants(Elem in) {
-  const int64_t tk = elem_bytes(in) ? 128 / elem_bytes(in) : 0;
-  if (tk == 0) return {};
-  if (in == Elem::F32) return {Variant{TileParams{128, 128, tk, 2, 32}, "tile128x128_wave64x64"}};
-  return {Variant{TileParams{128, 128, tk, 2, 16}, "tile128x128_wave64x32"}};
-}
-
-bool is_supported(const TileParams& t, Elem in) {
-  for (const Variant& v : supported_variants(in))
-    if (v.tiles.tile_m == t.tile_m && v.tiles.tile_n == t.tile_n && v.tiles.tile_k == t.tile_k &&
-        v.tiles.thread_tile_m == t.thread_tile_m && v.tiles.thread_tile_n == t.thread_tile_n)
-      return true;
-  return false;
-}
 
 // Regex reader of the five integer keys: first match wins, so a
 // best_summary.json with a nested "best" object parses too
@@ -98,55 +81,50 @@ bool write_best_json(const TileParams& t, const std::string& path, std::string& 
 }
 
 // ---------------------------------------------------------------------------
-// cost model
+// ranking
 // ---------------------------------------------------------------------------
-// Dense MFMA FLOP per clock per CU on gfx950 (f16/bf16 4096, fp8 8192,
-// f32 256).
-static double mfma_flop_per_clk_cu(Elem in) {
-  switch (in) {
-    case Elem::F16:
-    case Elem::BF16: return 4096.0;
-    case Elem::F8E4M3FN: return 8192.0;
-    case Elem::F32: return 256.0;
-    default: return 0.0;
-  }
-}
-
+// One candidate per kernel variant that can run the chain: its tiles, the
+// fused path and latency the calibrated cost model gives it (the same
+// ranking the launcher's AUTO path uses), and the HBM-side bytes of that
+// path in the reference's four columns (compiler/solver/WelderSolverCAPI.cpp:87-97):
+// A as streamed by every column tile, B as streamed by every row block, the
+// output as written (and, on the split path, re-read and rewritten), and the
+// f32 logits a fused path never writes.
 std::vector<Candidate> solve(const ChainSpec& s, int64_t /*max_connect_level*/,
                              const ArchInfo& arch) {
   std::vector<Candidate> out;
+  const int in_code = elem_to_dtype_code(s.in), out_code = elem_to_dtype_code(s.out);
+  if (in_code < 0 || out_code < 0) return out;
   const int64_t isz = elem_bytes(s.in), osz = elem_bytes(s.out);
-  for (const Variant& v : supported_variants(s.in)) {
-    const TileParams& t = v.tiles;
-    const int64_t nrb = (s.m + t.tile_m - 1) / t.tile_m;
-    const int64_t nt = (s.n + t.tile_n - 1) / t.tile_n;
-    const int64_t tiles = s.batch * nrb * nt;
-    // Exchange path: every tile resident, one per CU.  Split: two per CU.
-    const bool exchange = tiles <= arch.num_cu;
-    const int64_t resident = exchange ? arch.num_cu : 2 * arch.num_cu;
-    const int64_t waves = (tiles + resident - 1) / resident;
-    const double clk = arch.clock_ghz * 1e9;
-    const double tile_flops = 2.0 * (double)t.tile_m * (double)t.tile_n * (double)s.k;
-    // resident tiles share a CU when two are resident per CU
-    const double per_tile_s = tile_flops / (mfma_flop_per_clk_cu(s.in) * clk) * (exchange ? 1.0 : 2.0);
-    const double t_mfma = (double)waves * per_tile_s;
-    Candidate c;
-    c.tiles = t;
-    c.path = exchange ? "exchange" : "split";
-    c.bytes_a = s.batch * s.m * s.k * isz * nt;  // each column tile streams its A rows
-    c.bytes_b = s.batch * s.k * s.n * isz * nrb;
-    c.bytes_c = s.batch * s.m * s.n * osz * (exchange ? 1 : 3);  // split: write, re-read, re-write
-    c.bytes_cut = s.batch * s.m * s.n * 4;  // f32 logits never written to HBM
-    // HBM sees A and B once when the XCD L2s and the MALL catch the re-reads.
-    const double hbm_bytes = (double)(s.batch * (s.m * s.k + s.k * s.n) * isz) + (double)c.bytes_c;
-    const double t_hbm = hbm_bytes / (arch.hbm_gbs * 1e9);
-    const double t_softmax = exchange ? 2e-6 : 4e-6;  // row exchange vs second launch
-    c.estimated_latency = (std::max(t_mfma, t_hbm) + t_softmax) * 1e6;
-    c.score = 1.0 / c.estimated_latency;
-    out.push_back(c);
+  const Problem pr{s.batch, s.m, s.n, s.k, in_code, out_code, (int)arch.num_cu, 1};
+  const double flop = 2.0 * (double)s.batch * (double)s.m * (double)s.n * (double)s.k;
+  for (const VariantDesc& v : variants_for(in_code)) {
+    const std::vector<Choice> cs = rank_choices(pr, WTC_PATH_AUTO, v.id);
+    if (cs.empty()) continue;
+    const Choice& c = cs.front();
+    const int64_t nrb = (s.m + v.tile_rows - 1) / v.tile_rows;
+    const int64_t nt = (s.n + 127) / 128;
+    Candidate cand;
+    cand.tiles = TileParams{v.tile_m, v.tile_n, v.tile_k, v.thread_tile_m, v.thread_tile_n};
+    cand.variant = v.name;
+    cand.path = c.path == WTC_PATH_EXCHANGE ? "exchange" : (c.path == WTC_PATH_SPLIT ? "split" : "rows");
+    if (c.path == WTC_PATH_ROWS) {
+      // the row block's A stays in LDS; B streams once per pass
+      cand.bytes_a = s.batch * s.m * s.k * isz;
+      cand.bytes_b = s.batch * s.k * s.n * isz * nrb * 2;
+    } else {
+      cand.bytes_a = s.batch * s.m * s.k * isz * nt;
+      cand.bytes_b = s.batch * s.k * s.n * isz * nrb;
+    }
+    cand.bytes_c = s.batch * s.m * s.n * osz * (c.path == WTC_PATH_SPLIT ? 3 : 1);
+    cand.bytes_cut = s.batch * s.m * s.n * 4;
+    cand.estimated_latency = c.est_us;
+    cand.score = c.est_us > 0 ? flop / (c.est_us * 1e6) : 0.0;
+    out.push_back(cand);
   }
-  std::stable_sort(out.begin(), out.end(),
-                   [](const Candidate& a, const Candidate& b) { return a.score > b.score; });
+  std::stable_sort(out.begin(), out.end(), [](const Candidate& a, const Candidate& b) {
+    return a.estimated_latency < b.estimated_latency;
+  });
   return out;
 }
 
@@ -166,7 +144,8 @@ static bool write_best_summary(const ChainSpec& s, const ArchInfo& arch, const C
     << ", \"tileK\": " << best.tiles.tile_k << ", \"threadTileM\": " << best.tiles.thread_tile_m
     << ", \"threadTileN\": " << best.tiles.thread_tile_n << ", \"score\": " << best.score
     << ", \"estimatedLatency\": " << best.estimated_latency << ", \"profiledMs\": " << best.profiled_ms
-    << ", \"bytesCut\": " << best.bytes_cut << ", \"path\": \"" << best.path << "\"}\n";
+    << ", \"bytesCut\": " << best.bytes_cut << ", \"path\": \"" << best.path
+    << "\", \"variant\": \"" << best.variant << "\"}\n";
   o << "}\n";
   if (!write_file(path, o.str())) {
     err = "failed to open best summary json: " + path;
@@ -249,10 +228,12 @@ extern "C" int welder_solver_solve_typical_chain(
     return 4;
   }
   if (verbose) {
-    std::fprintf(stderr, "[wtc-solver] %zu candidate(s); best %lldx%lldx%lld (%s), est %.2f us\n",
-                 cs.size(), (long long)cs.front().tiles.tile_m, (long long)cs.front().tiles.tile_n,
-                 (long long)cs.front().tiles.tile_k, cs.front().path.c_str(),
-                 cs.front().estimated_latency);
+    for (size_t i = 0; i < cs.size(); ++i)
+      std::fprintf(stderr, "[wtc-solver] %zu: %s (%lldx%lldx%lld, lane %lldx%lld) on %s, est %.2f us\n",
+                   i, cs[i].variant.c_str(), (long long)cs[i].tiles.tile_m,
+                   (long long)cs[i].tiles.tile_n, (long long)cs[i].tiles.tile_k,
+                   (long long)cs[i].tiles.thread_tile_m, (long long)cs[i].tiles.thread_tile_n,
+                   cs[i].path.c_str(), cs[i].estimated_latency);
   }
   *out_tile_m = cs.front().tiles.tile_m;
   *out_tile_n = cs.front().tiles.tile_n;

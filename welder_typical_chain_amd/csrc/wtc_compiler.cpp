@@ -25,6 +25,7 @@
 #include <string>
 
 #include "chain_spec.h"
+#include "variants.h"
 #include "wtc/welder_compile_capi.h"
 #include "wtc/welder_solver_capi.h"
 
@@ -270,7 +271,13 @@ int run_pipeline(const Options& o) {
   }
   if (!have_best) {
     // search disabled and no tiles given: the library's default variant for the input type
-    best = wtc::supported_variants(spec.in).front().tiles;
+    const std::vector<wtc::VariantDesc> vs = wtc::variants_for(wtc::elem_to_dtype_code(spec.in));
+    if (vs.empty()) {
+      std::cerr << "wtc-compiler: no kernel variant for the chain's input type\n";
+      return 1;
+    }
+    best = wtc::TileParams{vs.front().tile_m, vs.front().tile_n, vs.front().tile_k,
+                           vs.front().thread_tile_m, vs.front().thread_tile_n};
     if (o.verbose) std::cout << "[wtc-compiler] no search: the default variant of the input type\n";
   }
   const fs::path best_path = search / "best.json";

@@ -35,19 +35,18 @@ struct ChainParams {
   uint64_t spin_ticks;  // exchange wait limit, 100 MHz ticks
 };
 
-// tile_rows: 128, or 256 for the split path with 16-bit or fp8 inputs; ks: 1,
-// or 2 for the k-split wave layout of 128-row tiles (exchange and split
-// epilogues, 16-bit and fp8 inputs).  NULL for a combination not built.
+// tile_rows: 128, or 256 (split epilogue, and f32 logits, with 16-bit or fp8
+// inputs); ks: 1, or 2 for the k-split wave layout of 128-row tiles
+// (exchange and split epilogues, and f32 logits, with 16-bit or fp8 inputs).
+// NULL for a combination not built.
 const void* chain_kernel_symbol(int in_dt, int out_dt, int epi, int tile_rows = 128, int ks = 1);
 const void* rescale_kernel_symbol(int out_dt);
 // Waves that share one row in rescale_rows_kernel (its grid is rows * wpr / 4).
 int rescale_waves_per_row(int64_t rows_total, int cu_count);
 const void* zero_kernel_symbol();
+// Static LDS of the exchange-epilogue kernel of this wave layout.
 int chain_kernel_lds_bytes(int in_dt, int out_dt, int ks = 1);
-// Tile height (128 or 256) the split path uses for this problem on a device
-// with cu_count compute units.
-int split_tile_rows(int in_dt, int64_t batch, int64_t m, int64_t n, int cu_count);
-int chain_kernel_threads(int in_dt);  // workgroup size of chain_tile_kernel
+int chain_kernel_threads(int in_dt);  // workgroup size of chain_tile_kernel (every layout)
 
 // One workgroup per 128-row block, two passes over N (K <= rows_kernel_max_k()).
 const void* rows_kernel_symbol(int in_dt, int out_dt);

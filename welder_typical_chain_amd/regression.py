@@ -134,14 +134,14 @@ def run_regression(out_base: Path, input_mlir: Path | None = None,
         s.require_contains("full_api_default.workgroup", d / "fused" / "04.kernel.plan.json",
                            r'"grid": \[\d+, \d+, \d+\], "block": \[\d+, \d+, \d+\]')
         s.require_contains("full_api_default.launchfunc", d / "fused" / "05.out.hip.launch.json",
-                           r'"entry": "wtc_matmul_softmax"')
+                           r'"entry": "wtc_matmul_softmax_tiles"')
 
         d = out_base / "pure_api_repeat"
         wtc("pure_api_repeat", "--input", input_mlir, "--output-dir", d, "--backend-mode", "api",
             "--pure-api-full", "--fused", "--repeat", pure_api_repeat)
         last = d / f"iter_{pure_api_repeat - 1}" / "fused" / "05.out.hip.launch.json"
         s.require_file("pure_api_repeat.runnable", last)
-        s.require_contains("pure_api_repeat.launchfunc", last, r'"entry": "wtc_matmul_softmax"')
+        s.require_contains("pure_api_repeat.launchfunc", last, r'"entry": "wtc_matmul_softmax_tiles"')
     except RegressionFailed:
         return 1
     print("[wtc] regression passed")

@@ -262,15 +262,19 @@ def run_case(launch: dict, *, pattern: str, seed: int, warmup: int, iters: int,
     # timed ones call the launcher C-ABI with its arguments marshalled once, as
     # the reference's profiler times back-to-back launches from C++
     # (WelderProfiler.cpp:752-792) without per-call host work of its own.
-    matmul_softmax(a, b, out=out, path=path, workspace=ws, logit_scale=scale)
+    # the manifest names the kernel variant (best.json's tiles) that runs
+    tiles = [int(launch["tiles"][key]) for key in ("tileM", "tileN", "tileK", "threadTileM",
+                                                   "threadTileN")]
+    matmul_softmax(a, b, out=out, path=path, workspace=ws, logit_scale=scale, tiles=tiles)
     from . import _lib
-    launch_fn = _lib.lib().wtc_matmul_softmax
+    launch_fn = _lib.lib().wtc_matmul_softmax_tiles
     in_code = {"f32": _lib.DTYPE_F32, "f16": _lib.DTYPE_F16, "bf16": _lib.DTYPE_BF16,
                "fp8": _lib.DTYPE_FP8_E4M3}[in_dt]
     out_code = {"f32": _lib.DTYPE_F32, "f16": _lib.DTYPE_F16, "bf16": _lib.DTYPE_BF16}[out_dt]
+    ctiles = _lib.Tiles(*tiles)
     call_args = (a.data_ptr(), b.data_ptr(), out.data_ptr(), batch, m, n, k, in_code, out_code,
-                 scale, 1.0, 1.0, _lib.PATHS[path], ws.data_ptr(), ws.numel(),
-                 torch.cuda.current_stream(dev).cuda_stream)
+                 scale, 1.0, 1.0, ctypes.byref(ctiles), _lib.PATHS[path], ws.data_ptr(),
+                 ws.numel(), torch.cuda.current_stream(dev).cuda_stream)
 
     def step():
         rc = launch_fn(*call_args)
