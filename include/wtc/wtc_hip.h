@@ -112,6 +112,19 @@ int wtc_matmul_softmax_tiles(const void *a, const void *b, void *out, int64_t ba
 int wtc_list_variants(int in_dtype, wtc_tiles *tiles, unsigned *paths,
                       const char **names, int capacity);
 
+/* Times one variant on one path on the current device: allocates A, B, out
+ * and a workspace, fills A and B with finite pseudo-random values (from
+ * `seed`), runs `warmup` untimed calls and then `iters` back-to-back calls
+ * between two HIP events on a stream of its own, frees everything and
+ * writes the mean microseconds per call.  `tiles` NULL = the cost model's
+ * choice.  The counterpart of the reference's profile step, which compiles
+ * and times top-ranked candidates with welder-profiler
+ * (backend/welder/compiler/solver/WelderSolverProfileCompileAndRun.h,
+ * WelderProfiler.cpp:752-792).  Synchronous; allocates. */
+int wtc_profile_tiles(int64_t batch, int64_t m, int64_t n, int64_t k, int in_dtype,
+                      int out_dtype, const wtc_tiles *tiles, int path, int warmup,
+                      int iters, uint64_t seed, double *us_per_call);
+
 /* Size of the device scratch array behind wtc_matmul_softmax_noalloc. */
 #define WTC_NOALLOC_SCRATCH_BYTES (8u << 20)
 

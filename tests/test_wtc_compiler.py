@@ -148,3 +148,21 @@ def test_reference_chain_files_full_pipeline(cli, tmp_path, fname):
     r = run(cli, "--input", REF_MLIR / fname, "--output-dir", out)
     assert r.returncode == 0, r.stderr
     assert (out / "fused" / "postbufferize_report.txt").is_file()
+
+
+def test_profiling_without_a_gpu_keeps_the_model_ranking(cli, c2_mlir, tmp_path):
+    """--enable-profiling on a host without a GPU: the first measurement
+    fails, the log says so, and the model's ranking and best.json stand."""
+    ref = tmp_path / "ref"
+    assert run(cli, "--input", c2_mlir, "--output-dir", ref, "--search-only").returncode == 0
+    out = tmp_path / "prof"
+    r = run(cli, "--input", c2_mlir, "--output-dir", out, "--search-only", "--enable-profiling",
+            "--profile-top-k", "2", "--profile-iters", "5")
+    assert r.returncode == 0, r.stderr
+    log = (out / "search" / "profile.log").read_text()
+    assert "rc=" in log and "model ranking kept" in log
+    assert (out / "search" / "best.json").read_text() == (ref / "search" / "best.json").read_text()
+    assert (out / "search" / "candidates.tsv").read_text() == \
+        (ref / "search" / "candidates.tsv").read_text()
+    bad = run(cli, "--input", c2_mlir, "--output-dir", out, "--profile-iters", "0")
+    assert bad.returncode == 2 and "positive integer" in bad.stderr

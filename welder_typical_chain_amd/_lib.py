@@ -60,6 +60,9 @@ SIGNATURES = {
                                                 ctypes.c_int, ctypes.c_int, ctypes.c_float,
                                                 ctypes.c_float, ctypes.c_float, _c_tiles,
                                                 ctypes.c_int, _c_p, ctypes.c_size_t, _c_p]),
+    "wtc_profile_tiles": (ctypes.c_int, [_c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_int, ctypes.c_int,
+                                         _c_tiles, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                         ctypes.c_uint64, ctypes.POINTER(ctypes.c_double)]),
     "wtc_list_variants": (ctypes.c_int, [ctypes.c_int, _c_tiles, ctypes.POINTER(ctypes.c_uint),
                                          ctypes.POINTER(ctypes.c_char_p), ctypes.c_int]),
     "wtc_plan_tiles": (ctypes.c_int, [_c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_int, ctypes.c_int,

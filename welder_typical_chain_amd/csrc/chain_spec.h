@@ -78,6 +78,11 @@ struct ArchInfo {
 };
 std::vector<Candidate> solve(const ChainSpec& spec, int64_t max_connect_level,
                              const ArchInfo& arch);
+// best_summary.json and candidates.tsv in the reference's formats
+// (backend/welder/compiler/solver/WelderSolverCAPI.cpp:40-97).
+bool write_best_summary(const ChainSpec& s, const ArchInfo& arch, const Candidate& best,
+                        const std::string& path, std::string& err);
+bool write_candidates(const std::vector<Candidate>& cs, const std::string& path, std::string& err);
 
 // ---- misc ---------------------------------------------------------------------
 bool read_file(const std::string& path, std::string& out);

@@ -414,6 +414,34 @@ int matmul_softmax_impl(const void* a, const void* b, void* out, int64_t batch, 
                         float scale_a, float scale_b, const wtc_tiles* tiles, int path,
                         void* workspace, size_t workspace_bytes, void* stream_, bool noalloc);
 
+// Profiling inputs: element i of a buffer of `dtype` from a hash of (seed, i),
+// finite and within +-2 (f32, f16, bf16: sign, an exponent of 2^-7 .. 2^0 and
+// random mantissa bits; fp8 e4m3: exponent field 1 .. 8, never the NaN code).
+__global__ void fill_random_kernel(uint8_t* p, int64_t count, int dtype, uint64_t seed) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += stride) {
+    uint64_t h = seed ^ ((uint64_t)i * 0x9E3779B97F4A7C15ull);
+    h ^= h >> 31;
+    h *= 0xBF58476D1CE4E5B9ull;
+    h ^= h >> 29;
+    const uint32_t r = (uint32_t)(h >> 16);
+    const uint32_t sign = r >> 31, mant = r & 0x7FFFFFu, ex = (r >> 23) & 7u;
+    if (dtype == DT_FP8) {
+      p[i] = (uint8_t)((sign << 7) | ((ex + 1u) << 3) | (mant & 7u));
+      continue;
+    }
+    const uint32_t bits = (sign << 31) | ((127u - 7u + ex) << 23) | mant;
+    if (dtype == DT_F32) {
+      reinterpret_cast<uint32_t*>(p)[i] = bits;
+    } else if (dtype == DT_BF16) {
+      reinterpret_cast<uint16_t*>(p)[i] = (uint16_t)(bits >> 16);
+    } else {  // f16: exponent 15 - 7 + ex, top ten mantissa bits
+      reinterpret_cast<uint16_t*>(p)[i] =
+          (uint16_t)((sign << 15) | ((15u - 7u + ex) << 10) | (mant >> 13));
+    }
+  }
+}
+
 }  // namespace
 
 extern "C" {
@@ -444,6 +472,88 @@ int wtc_plan_tiles(int64_t batch, int64_t m, int64_t n, int64_t k, int in_dtype,
   if (workspace_bytes) *workspace_bytes = pl.ws;
   if (estimated_us) *estimated_us = pl.est_us;
   return WTC_OK;
+}
+
+int wtc_profile_tiles(int64_t batch, int64_t m, int64_t n, int64_t k, int in_dtype, int out_dtype,
+                      const wtc_tiles* tiles, int path, int warmup, int iters, uint64_t seed,
+                      double* us_per_call) {
+  g_last_error.clear();
+  if (!us_per_call) return fail(WTC_ERR_ARG, "us_per_call is NULL");
+  if (iters <= 0 || warmup < 0) return fail(WTC_ERR_ARG, "iters must be positive, warmup >= 0");
+  int rc = check_args(batch, m, n, k, in_dtype, out_dtype, path);
+  if (rc) return rc;
+  if (batch == 0 || m == 0 || n == 0) return fail(WTC_ERR_ARG, "empty problem");
+  int dev = 0;
+  HIP_TRY(hipGetDevice(&dev));
+  int cu = 0, occ = 1;
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    DeviceState* ds = nullptr;
+    rc = device_state(dev, &ds);
+    if (rc) return rc;
+    cu = ds->cu_count;
+    occ = ds->occ[in_dtype][out_dtype];
+  }
+  Plan pl;
+  rc = plan_impl(batch, m, n, k, in_dtype, out_dtype, path, tiles, cu, occ, &pl);
+  if (rc) return rc;
+  const int64_t isz = dtype_bytes(in_dtype), osz = dtype_bytes(out_dtype);
+  const size_t a_bytes = (size_t)(batch * m * k * isz), b_bytes = (size_t)(batch * k * n * isz);
+  const size_t o_bytes = (size_t)(batch * m * n * osz), w_bytes = (size_t)pl.ws;
+  void *a = nullptr, *b = nullptr, *o = nullptr, *w = nullptr;
+  hipStream_t st = nullptr;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  auto release = [&]() {
+    if (st) (void)hipStreamSynchronize(st);
+    for (void* q : {a, b, o, w})
+      if (q) (void)hipFree(q);
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    if (st) (void)hipStreamDestroy(st);
+  };
+  auto run = [&]() -> int {
+    HIP_TRY(hipMalloc(&a, a_bytes ? a_bytes : 16));
+    HIP_TRY(hipMalloc(&b, b_bytes ? b_bytes : 16));
+    HIP_TRY(hipMalloc(&o, o_bytes));
+    HIP_TRY(hipMalloc(&w, w_bytes));
+    HIP_TRY(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
+    HIP_TRY(hipEventCreate(&e0));
+    HIP_TRY(hipEventCreate(&e1));
+    int r = zero_fill(w, (int64_t)w_bytes, st);
+    if (r) return r;
+    const struct { void* p; int64_t count; uint64_t salt; } fills[] = {
+        {a, batch * m * k, 0x5851F42D4C957F2Dull}, {b, batch * k * n, 0x14057B7EF767814Full}};
+    for (const auto& f : fills) {
+      if (f.count == 0) continue;
+      uint8_t* ptr = static_cast<uint8_t*>(f.p);
+      int64_t count = f.count;
+      int dt = in_dtype;
+      uint64_t sd = seed ^ f.salt;
+      void* args[] = {&ptr, &count, &dt, &sd};
+      HIP_TRY(hipLaunchKernel(reinterpret_cast<const void*>(&fill_random_kernel), dim3(1024),
+                              dim3(256), args, 0, st));
+    }
+    for (int i = 0; i < warmup + iters; ++i) {
+      if (i == warmup) HIP_TRY(hipEventRecord(e0, st));
+      r = matmul_softmax_impl(a, b, o, batch, m, n, k, in_dtype, out_dtype, 1.0f, 1.0f, 1.0f,
+                              tiles, path, w, w_bytes, st, false);
+      if (r) return r;
+    }
+    HIP_TRY(hipEventRecord(e1, st));
+    HIP_TRY(hipEventSynchronize(e1));
+    float ms = 0.0f;
+    HIP_TRY(hipEventElapsedTime(&ms, e0, e1));
+    *us_per_call = (double)ms * 1e3 / iters;
+    std::lock_guard<std::mutex> lk(g_mu);
+    DeviceState* ds = nullptr;
+    r = device_state(dev, &ds);
+    return r ? r : take_mailbox(ds);
+  };
+  rc = run();
+  const std::string msg = g_last_error;
+  release();
+  g_last_error = msg;
+  return rc;
 }
 
 int wtc_list_variants(int in_dtype, wtc_tiles* tiles, unsigned* paths, const char** names,

@@ -128,7 +128,7 @@ std::vector<Candidate> solve(const ChainSpec& s, int64_t /*max_connect_level*/,
   return out;
 }
 
-static bool write_best_summary(const ChainSpec& s, const ArchInfo& arch, const Candidate& best,
+bool write_best_summary(const ChainSpec& s, const ArchInfo& arch, const Candidate& best,
                                const std::string& path, std::string& err) {
   std::error_code ec;
   const auto parent = std::filesystem::path(path).parent_path();
@@ -155,7 +155,7 @@ static bool write_best_summary(const ChainSpec& s, const ArchInfo& arch, const C
 }
 
 // 13 columns, as backend/welder/compiler/solver/WelderSolverCAPI.cpp:87-97.
-static bool write_candidates(const std::vector<Candidate>& cs, const std::string& path,
+bool write_candidates(const std::vector<Candidate>& cs, const std::string& path,
                              std::string& err) {
   std::error_code ec;
   const auto parent = std::filesystem::path(path).parent_path();

@@ -17,17 +17,20 @@
 // --compile-only (the reference's semantics: search only when no tiles are given).
 // --backend-root / --backend-mode / --pure-api-full are accepted for
 // compatibility; there is one in-process backend.
+#include <algorithm>
 #include <cstdint>
 #include <cstdlib>
 #include <filesystem>
 #include <iostream>
 #include <sstream>
 #include <string>
+#include <vector>
 
 #include "chain_spec.h"
 #include "variants.h"
 #include "wtc/welder_compile_capi.h"
 #include "wtc/welder_solver_capi.h"
+#include "wtc/wtc_hip.h"
 
 namespace {
 
@@ -48,6 +51,9 @@ struct Options {
   bool pure_api_full = false;
   Mode mode = Mode::Full;
   bool verbose = false;
+  // measure the top-ranked candidates on the GPU and keep the fastest
+  bool enable_profiling = false;
+  int64_t profile_top_k = 4, profile_warmup = 20, profile_iters = 200;
 };
 
 int count_of(const std::string& text, const char* needle) {
@@ -183,6 +189,54 @@ bool validate(const fs::path& dir, std::string& diag) {
   return true;
 }
 
+// The profile step: time the first `profile_top_k` candidates of the model's
+// ranking on the current device (wtc_profile_tiles), put the measured ones
+// first, fastest first, and rewrite the search outputs.  A failed
+// measurement (no GPU, say) ends the step and keeps the model's ranking, as
+// the reference falls back to its heuristic cost for a candidate that fails
+// to compile or profile unless told to prune it
+// (backend/welder/compiler/driver/WelderCompilerCliOptions.h:333-336).
+bool profile_candidates(const Options& o, const wtc::ChainSpec& spec, const fs::path& summary,
+                        const fs::path& candidates, const fs::path& search, wtc::TileParams& best) {
+  wtc::ArchInfo arch;
+  std::vector<wtc::Candidate> cs = wtc::solve(spec, o.max_connect_level, arch);
+  const int in = wtc::elem_to_dtype_code(spec.in), out = wtc::elem_to_dtype_code(spec.out);
+  std::ostringstream log;
+  size_t measured = 0;
+  for (size_t i = 0; i < cs.size() && (int64_t)i < o.profile_top_k; ++i) {
+    const wtc::TileParams& t = cs[i].tiles;
+    const wtc_tiles tiles{t.tile_m, t.tile_n, t.tile_k, t.thread_tile_m, t.thread_tile_n};
+    const int path = cs[i].path == "exchange" ? WTC_PATH_EXCHANGE
+                     : cs[i].path == "split"  ? WTC_PATH_SPLIT
+                                              : WTC_PATH_ROWS;
+    double us = 0;
+    const int rc = wtc_profile_tiles(spec.batch, spec.m, spec.n, spec.k, in, out, &tiles, path,
+                                     (int)o.profile_warmup, (int)o.profile_iters, 0x5EEDull + i, &us);
+    log << "[wtc.profile] " << cs[i].variant << " " << cs[i].path << " rc=" << rc;
+    if (rc != 0) {
+      log << " error=" << wtc_last_error() << " (model ranking kept from here on)\n";
+      break;
+    }
+    log << " us=" << us << " estimated_us=" << cs[i].estimated_latency << "\n";
+    cs[i].profiled_ms = us / 1000.0;
+    ++measured;
+  }
+  wtc::write_file((search / "profile.log").string(), log.str());
+  if (o.verbose) std::cout << log.str();
+  if (measured == 0) return true;
+  std::stable_sort(cs.begin(), cs.begin() + measured, [](const wtc::Candidate& a, const wtc::Candidate& b) {
+    return a.profiled_ms < b.profiled_ms;
+  });
+  std::string err;
+  if (!wtc::write_best_summary(spec, arch, cs.front(), summary.string(), err) ||
+      !wtc::write_candidates(cs, candidates.string(), err)) {
+    std::cerr << "wtc-compiler: " << err << "\n";
+    return false;
+  }
+  best = cs.front().tiles;
+  return true;
+}
+
 bool any_override(const wtc::TileParams& t) {
   return t.tile_m > 0 || t.tile_n > 0 || t.tile_k > 0 || t.thread_tile_m > 0 ||
          t.thread_tile_n > 0;
@@ -254,6 +308,8 @@ int run_pipeline(const Options& o) {
     if (o.verbose) {
       std::cout << "[wtc-compiler] ranked candidates in " << candidates.string() << "\n";
     }
+    if (o.enable_profiling && !profile_candidates(o, spec, summary, candidates, search, best))
+      return 1;
   }
   if (any_override(o.override_tiles)) {
     if (o.verbose) std::cout << "[wtc-compiler] tiles overridden on the command line\n";
@@ -332,6 +388,10 @@ void usage() {
             << "  --best-json FILE          tileM/tileN/tileK/threadTileM/threadTileN from a JSON file\n"
             << "  --tile-m N  --tile-n N  --tile-k N  --thread-tile-m N  --thread-tile-n N\n"
             << "  --max-connect-level N     recorded in the plan (the fused kernel needs none)\n"
+            << "profiling (needs a GPU; the ranking stays the model's where it fails):\n"
+            << "  --enable-profiling        time the first candidates on the device, rank them by\n"
+            << "                            measured time (candidates.tsv profiledMs), keep the fastest\n"
+            << "  --profile-top-k N  --profile-warmup N  --profile-iters N   (4, 20, 200)\n"
             << "accepted and ignored (a single in-process backend):\n"
             << "  --backend-root DIR  --legacy-root DIR  --backend-mode MODE  --pure-api-full\n"
             << "output layout: DIR/ir (01, 02), DIR/search (best.json, best_summary.json,\n"
@@ -405,6 +465,17 @@ int main(int argc, char** argv) {
       if (o.max_connect_level > 0) o.max_connect_level = 0;
     } else if (arg == "--fused") {
       o.fused = true;
+    } else if (arg == "--enable-profiling") {
+      o.enable_profiling = true;
+    } else if ((arg == "--profile-top-k" || arg == "--profile-warmup" || arg == "--profile-iters") &&
+               has_value) {
+      int64_t v = 0;
+      if (!parse_int(argv[++i], v) || v < (arg == "--profile-warmup" ? 0 : 1)) {
+        std::cerr << "wtc-compiler: " << arg << " needs a positive integer\n";
+        return 2;
+      }
+      (arg == "--profile-top-k" ? o.profile_top_k
+                                : (arg == "--profile-warmup" ? o.profile_warmup : o.profile_iters)) = v;
     } else if (arg == "--verbose") {
       o.verbose = true;
     } else if (arg == "--help" || arg == "-h") {
