@@ -54,25 +54,66 @@ def parse():
     return ap.parse_args()
 
 
+def host_info():
+    """The host the CPU baseline runs on: nproc (processing units this process
+    may use, as GNU nproc counts them), logical CPUs, CPU model (lscpu)."""
+    import subprocess
+    info = {"logical_cpus": os.cpu_count(), "affinity_cpus": len(os.sched_getaffinity(0))}
+    try:
+        info["nproc"] = int(subprocess.run(["nproc"], capture_output=True, text=True,
+                                           timeout=10).stdout.strip())
+    except (OSError, ValueError, subprocess.SubprocessError):
+        info["nproc"] = info["affinity_cpus"]
+    model = None
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        model = next((ln.split(":", 1)[1].strip() for ln in out.splitlines()
+                      if ln.startswith("Model name")), None)
+    except (OSError, subprocess.SubprocessError):
+        pass
+    info["model"] = model
+    return info
+
+
 def cpu_baseline(a_host, b_host, n, k, budget_s):
-    """f32 loops restatement of the reference CPU path on a bounded row sample."""
+    """The chain lowered to f32 loops (oracle/wtc_oracle.c built with ROCm's
+    clang -O3 and LLVM OpenMP, the restatement of the reference's mlir-opt CPU
+    path): C2 on all `nproc` cores (all 2048 rows when the budget allows, else
+    a row sample), C2 on one core (a row sample, extrapolated), and C1 in
+    full on one core and on all cores."""
     from oracle import oracle as O
-    threads = min(O.cpu_max_threads(), int(os.environ.get("OMP_NUM_THREADS", "16") or 16))
-    _, t1 = O.cpu_chain_loops(a_host, b_host, 0, threads, threads)  # calibration: one row per thread
-    per_row = max(t1 / 1.0, 1e-6)   # seconds per `threads` rows
-    rows = max(threads, int(budget_s / per_row) * threads)
-    rows = min(rows, a_host.shape[0])
-    _, secs = O.cpu_chain_loops(a_host, b_host, 0, rows, threads)
+    from welder_typical_chain_amd.configs import CONFIGS
+    host = host_info()
+    threads = max(1, host["nproc"])
+    rows_total = a_host.shape[0]
+    # calibration: one row per thread
+    _, t_cal = O.cpu_chain_loops(a_host, b_host, 0, threads, threads, baseline=True)
+    per_row_all = max(t_cal / threads, 1e-9)
+    rows = min(rows_total, max(threads, int(budget_s / 2 / per_row_all) // threads * threads))
+    _, secs = O.cpu_chain_loops(a_host, b_host, 0, rows, threads, baseline=True)
     tflops = 2.0 * rows * n * k / secs / 1e12
-    # the same loops on one core (the loops lowering runs single-threaded),
-    # on a smaller sample: about a quarter of the budget, at least 8 rows
-    rows1 = min(a_host.shape[0], max(8, int(budget_s / 4 / per_row)))
-    _, secs1 = O.cpu_chain_loops(a_host, b_host, 0, rows1, 1)
-    return {"value": tflops, "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "sample": f"{rows} of 2048 rows of C2 (f32 i-j-k loops + max/exp/sum/div, "
-                      f"OpenMP over rows), {secs:.1f} s",
-            "single_thread": {"value": 2.0 * rows1 * n * k / secs1 / 1e12, "cores": 1,
-                              "sample": f"{rows1} rows, {secs1:.1f} s"}}
+    _, t_one = O.cpu_chain_loops(a_host, b_host, 0, 1, 1, baseline=True)
+    rows1 = min(rows_total, max(4, int(budget_s / 3 / max(t_one, 1e-9))))
+    _, secs1 = O.cpu_chain_loops(a_host, b_host, 0, rows1, 1, baseline=True)
+    # C1 in full (128 rows), median of repeated runs
+    c1 = CONFIGS["C1"]
+    inp = O.make_inputs(c1, seed=0)
+    a1, b1 = inp.a[0], inp.b[0]
+    c1_us = {}
+    for label, th in (("single_thread", 1), ("all_cores", threads)):
+        runs = sorted(O.cpu_chain_loops(a1, b1, 0, c1.m, th, baseline=True)[1] for _ in range(15))
+        c1_us[label] = round(runs[len(runs) // 2] * 1e6, 1)
+    return {"value": round(tflops, 6), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": (f"C2 {'all' if rows == rows_total else rows} of {rows_total} rows "
+                       f"(f32 i-j-k loops + max/exp/sum/div, OpenMP over rows on {threads} threads), "
+                       f"{secs:.2f} s"),
+            "compiler": "ROCm clang -O3 -fopenmp (LLVM CPU backend)",
+            "host": host, "threads": threads,
+            "single_thread": {"value": round(2.0 * rows1 * n * k / secs1 / 1e12, 6), "cores": 1,
+                              "sample": f"C2 {rows1} rows, {secs1:.2f} s",
+                              "c2_full_s_extrapolated": round(secs1 * rows_total / rows1, 2)},
+            "c1_full_us": {**c1_us, "flop": c1.flops,
+                           "problem": "C1 f32 128x128 . 128x128, uniform[-1,1], seed 0"}}
 
 
 PEAKS = {"f16": PEAK_F16_TFLOPS, "bf16": PEAK_F16_TFLOPS, "fp8": 5000.0}
@@ -110,19 +151,25 @@ PROFILED_PATH = {"C2": "exchange", "C3": "rows", "C4": "split", "C5": "split"}
 
 
 def load_traffic(workload: str = "C2", path: str = "auto"):
-    """HBM bytes per launch of the workload's dominant kernel, from the committed
-    rocprofv3 FETCH_SIZE / WRITE_SIZE summaries (None if absent, or if this run
-    takes another path than the one profiled)."""
+    """(HBM bytes per launch of the workload's dominant kernel, provenance)
+    from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summaries.  The
+    bytes are None if absent or if this run takes another path than the one
+    profiled; the provenance names the summary, the source digest of the
+    build it measured and of the build in this tree, so a stale figure shows."""
+    from welder_typical_chain_amd.build import build_info
+    this = build_info().get("source_digest")
     if path not in ("auto", PROFILED_PATH.get(workload)):
-        return None
+        return None, {"file": None, "this_build": this, "reason": "path not profiled"}
+    name = "c2_f16_exchange_traffic.json" if workload == "C2" else "c3_c4_c5_traffic.json"
     try:
-        if workload == "C2":
-            p = ROOT / "profiles" / "c2_f16_exchange_traffic.json"
-            return json.loads(p.read_text()).get("hbm_bytes_per_launch")
-        p = ROOT / "profiles" / "c3_c4_c5_traffic.json"
-        return json.loads(p.read_text())["workloads"][workload]["hbm_bytes_per_launch"]
+        doc = json.loads((ROOT / "profiles" / name).read_text())
+        rec = doc if workload == "C2" else doc["workloads"][workload]
+        built = doc.get("profile_build", {}).get("source_digest")
+        return rec.get("hbm_bytes_per_launch"), {
+            "file": f"profiles/{name}", "profile_build": built, "this_build": this,
+            "same_build": built is not None and built == this}
     except (OSError, ValueError, KeyError):
-        return None
+        return None, {"file": None, "this_build": this, "reason": "no summary"}
 
 
 def main():
@@ -231,6 +278,7 @@ def main():
         cpu = cpu_baseline(a.float().cpu().numpy(), b.float().cpu().numpy(), n, k, args.cpu_seconds)
 
     peak = PEAKS[cfg.in_dtype]
+    traffic, traffic_src = load_traffic(args.workload, args.path)
     alg_bytes = (a.numel() * a.element_size() + b.numel() * b.element_size() +
                  out.numel() * out.element_size())
     gbs = alg_bytes / (ms * 1e-3) / 1e9
@@ -247,11 +295,11 @@ def main():
                        "in_dtype": cfg.in_dtype, "out_dtype": cfg.out_dtype, "path": args.path},
             "roofline": ({"bound": "mfma", "achieved": round(tflops, 3), "peak": peak,
                           "unit": "TFLOP/s", "frac": round(tflops / peak, 4),
-                          "traffic": load_traffic(args.workload, args.path)}
+                          "traffic": traffic, "traffic_profile": traffic_src}
                          if mfma_bound else
                          {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
                           "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
-                          "traffic": load_traffic(args.workload, args.path)}),
+                          "traffic": traffic, "traffic_profile": traffic_src}),
             "launch": launch_info,
             "checks": {"row_sum_max_dev": row_dev, "device_error_flags": flags},
         }
@@ -276,7 +324,7 @@ def main():
                    "batch": 1, "accumulate": "f32", "out_dtype": "f16", "path": args.path},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 3), "peak": PEAK_F16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tflops / PEAK_F16_TFLOPS, 4),
-                     "traffic": load_traffic("C2", args.path)},
+                     "traffic": traffic, "traffic_profile": traffic_src},
         "cpu_baseline": cpu,
         "launch": launch_info,
         "checks": {"row_sum_max_dev": row_dev, "device_error_flags": flags,

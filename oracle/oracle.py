@@ -16,6 +16,9 @@ import numpy as np
 
 HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "_build" / "libwtc_oracle.so"
+# the same source built with ROCm's clang -O3 and LLVM's OpenMP: the loops
+# bench.py times as the CPU baseline
+BASELINE_LIB_PATH = HERE / "_build" / "libwtc_cpu_baseline.so"
 
 _lib = None
 
@@ -60,18 +63,33 @@ def build() -> Path:
     return LIB_PATH
 
 
+def _load(path: Path) -> ctypes.CDLL:
+    if not path.exists():
+        build()
+    h = ctypes.CDLL(str(path))
+    for name, (res, args) in _SIGS.items():
+        fn = getattr(h, name)
+        fn.restype = res
+        fn.argtypes = args
+    return h
+
+
 def lib() -> ctypes.CDLL:
     global _lib
     if _lib is None:
-        if not LIB_PATH.exists():
-            build()
-        h = ctypes.CDLL(str(LIB_PATH))
-        for name, (res, args) in _SIGS.items():
-            fn = getattr(h, name)
-            fn.restype = res
-            fn.argtypes = args
-        _lib = h
+        _lib = _load(LIB_PATH)
     return _lib
+
+
+_baseline_lib = None
+
+
+def baseline_lib() -> ctypes.CDLL:
+    """The clang -O3 build (CPU baseline timing only)."""
+    global _baseline_lib
+    if _baseline_lib is None:
+        _baseline_lib = _load(BASELINE_LIB_PATH)
+    return _baseline_lib
 
 
 def _p(arr: np.ndarray, ptype):
@@ -187,21 +205,24 @@ def chain_rows_f16acc(a: np.ndarray, b: np.ndarray, rows) -> np.ndarray:
     return probs
 
 
-def cpu_chain_loops(a: np.ndarray, b: np.ndarray, row0: int, nrows: int, threads: int = 1):
-    """The chain lowered to loops in f32 on rows [row0, row0+nrows); returns (out, seconds)."""
+def cpu_chain_loops(a: np.ndarray, b: np.ndarray, row0: int, nrows: int, threads: int = 1,
+                    baseline: bool = False):
+    """The chain lowered to loops in f32 on rows [row0, row0+nrows); returns
+    (out, seconds).  baseline=True runs the clang -O3 build."""
     a = np.ascontiguousarray(a, np.float32)
     b = np.ascontiguousarray(b, np.float32)
     k = a.shape[1]
     n = b.shape[1]
     c = np.empty((nrows, n), np.float32)
     out = np.empty((nrows, n), np.float32)
-    secs = lib().wtc_cpu_chain_loops_f32(_p(a, _f32p), _p(b, _f32p), _p(c, _f32p), _p(out, _f32p),
-                                         n, k, row0, nrows, threads)
+    h = baseline_lib() if baseline else lib()
+    secs = h.wtc_cpu_chain_loops_f32(_p(a, _f32p), _p(b, _f32p), _p(c, _f32p), _p(out, _f32p),
+                                     n, k, row0, nrows, threads)
     return out, float(secs)
 
 
-def cpu_max_threads() -> int:
-    return int(lib().wtc_cpu_max_threads())
+def cpu_max_threads(baseline: bool = False) -> int:
+    return int((baseline_lib() if baseline else lib()).wtc_cpu_max_threads())
 
 
 # ------------------------------------------------------------------- inputs

@@ -34,6 +34,7 @@ COMPILE_LIB = PKG / "libwelder-compile-capi.so"
 SOLVER_LIB = PKG / "libwelder-solver-capi.so"
 CLI = PKG / "wtc-compiler"
 RESOURCES = PKG / "kernel_resources.json"
+BUILD_INFO = PKG / "build_info.json"
 RESOURCES_TSV = PKG / "kernel_resources.tsv"
 TSV_COLUMNS = ["vgpr_count", "agpr_count", "sgpr_count", "vgpr_spill_count", "sgpr_spill_count",
                "lds_bytes", "scratch_bytes", "mfma", "lds_dma_loads", "ds_read_tr", "scratch_ops",
@@ -141,6 +142,43 @@ def _kernel_resources(code_objects: list[Path]) -> dict:
     return {"target": ARCH, "kernels": kernels}
 
 
+def source_digest() -> str:
+    """SHA-256 over the sources a build compiles (csrc/ and include/wtc/),
+    in name order: the stamp that ties a measurement to the build it ran."""
+    import hashlib
+    h = hashlib.sha256()
+    files = sorted([*CSRC.glob("*.hip"), *CSRC.glob("*.cpp"), *CSRC.glob("*.h"),
+                    *(ROOT / "include" / "wtc").glob("*.h")])
+    for f in files:
+        h.update(f.name.encode() + b"\0" + f.read_bytes() + b"\0")
+    return h.hexdigest()[:16]
+
+
+def _write_build_info() -> None:
+    import json
+    info = {"source_digest": source_digest()}
+    try:
+        head = subprocess.run(["git", "-C", str(ROOT), "rev-parse", "--short", "HEAD"],
+                              capture_output=True, text=True, timeout=10)
+        dirty = subprocess.run(["git", "-C", str(ROOT), "status", "--porcelain", "--", "include",
+                                str(CSRC)], capture_output=True, text=True, timeout=10)
+        if head.returncode == 0:
+            info["git_head"] = head.stdout.strip()
+            info["sources_changed_since_head"] = bool(dirty.stdout.strip())
+    except (OSError, subprocess.SubprocessError):
+        pass
+    BUILD_INFO.write_text(json.dumps(info, indent=1) + "\n")
+
+
+def build_info() -> dict:
+    """The stamp of the library in this tree ({} if it was never built)."""
+    import json
+    try:
+        return json.loads(BUILD_INFO.read_text())
+    except (OSError, ValueError):
+        return {}
+
+
 def build(verbose: bool = False) -> Path:
     """Compile every source (always; no staleness shortcut) and link."""
     import json
@@ -174,6 +212,7 @@ def build(verbose: bool = False) -> Path:
     for name, k in sorted(res["kernels"].items()):
         rows.append("\t".join([name, k["code_object"], *(str(k.get(c, 0)) for c in TSV_COLUMNS)]))
     RESOURCES_TSV.write_text("\n".join(rows) + "\n")
+    _write_build_info()
     if verbose:
         print(f"built {LIB}")
     return LIB
