@@ -164,8 +164,8 @@ int plan_impl(int64_t batch, int64_t m, int64_t n, int64_t k, int in_dt, int out
     vid = v.id;
   }
   const Problem pr{batch, m, n, k, in_dt, out_dt, cu_count, xch_per_cu};
-  const std::vector<Choice> cs = rank_choices(pr, path, vid);
-  if (cs.empty()) {
+  Choice c{};
+  if (!best_choice(pr, path, vid, &c)) {
     // the reason of the first variant that implements the path asked for
     std::string why = "no kernel variant runs this problem";
     for (const VariantDesc& d : variants_for(in_dt)) {
@@ -179,7 +179,6 @@ int plan_impl(int64_t batch, int64_t m, int64_t n, int64_t k, int in_dt, int out
     }
     return fail(WTC_ERR_UNSUPPORTED, why);
   }
-  const Choice& c = cs.front();
   const int64_t grid = variant_grid(c.v, c.path, pr);
   if (grid > 0x7FFFFFFFll) return fail(WTC_ERR_UNSUPPORTED, "too many tiles for one grid");
   out->v = c.v;
@@ -188,6 +187,57 @@ int plan_impl(int64_t batch, int64_t m, int64_t n, int64_t k, int in_dt, int out
   out->ws = ws_layout(batch, m, n, c.path).total;
   out->est_us = c.est_us;
   return WTC_OK;
+}
+
+// Recent plans of the launch path, keyed by everything plan_impl reads:
+// callers repeat shapes, and ranking the variants on every call costs a few
+// microseconds of host time.  Guarded by g_mu.
+struct PlanKey {
+  int64_t batch, m, n, k;
+  int in_dt, out_dt, path, cu, occ;
+  int64_t tiles[5];  // all zero: no variant given
+  bool operator==(const PlanKey& o) const { return std::memcmp(this, &o, sizeof *this) == 0; }
+};
+struct PlanCache {
+  static constexpr int kSize = 16;
+  PlanKey key[kSize];
+  Plan plan[kSize];
+  int used = 0, next = 0;
+  const Plan* find(const PlanKey& k) const {
+    for (int i = 0; i < used; ++i)
+      if (key[i] == k) return &plan[i];
+    return nullptr;
+  }
+  void put(const PlanKey& k, const Plan& p) {
+    key[next] = k;
+    plan[next] = p;
+    next = (next + 1) % kSize;
+    if (used < kSize) ++used;
+  }
+};
+PlanCache g_plans;
+
+PlanKey plan_key(int64_t batch, int64_t m, int64_t n, int64_t k, int in_dt, int out_dt, int path,
+                 const wtc_tiles* tiles, int cu, int occ) {
+  PlanKey key;
+  std::memset(&key, 0, sizeof key);  // padding too: keys compare bytewise
+  key.batch = batch;
+  key.m = m;
+  key.n = n;
+  key.k = k;
+  key.in_dt = in_dt;
+  key.out_dt = out_dt;
+  key.path = path;
+  key.cu = cu;
+  key.occ = occ;
+  if (tiles) {
+    key.tiles[0] = tiles->tile_m;
+    key.tiles[1] = tiles->tile_n;
+    key.tiles[2] = tiles->tile_k;
+    key.tiles[3] = tiles->thread_tile_m;
+    key.tiles[4] = tiles->thread_tile_n;
+  }
+  return key;
 }
 
 // A default workspace of one stream.  Grow-only: a superseded buffer is kept
@@ -690,9 +740,16 @@ int matmul_softmax_impl(const void* a, const void* b, void* out, int64_t batch, 
   if (rc) return rc;
 
   Plan pl;
-  rc = plan_impl(batch, m, n, k, in_dtype, out_dtype, path, tiles, ds->cu_count,
-                 ds->occ[in_dtype][out_dtype], &pl);
-  if (rc) return rc;
+  const PlanKey key = plan_key(batch, m, n, k, in_dtype, out_dtype, path, tiles, ds->cu_count,
+                               ds->occ[in_dtype][out_dtype]);
+  if (const Plan* hit = g_plans.find(key)) {
+    pl = *hit;
+  } else {
+    rc = plan_impl(batch, m, n, k, in_dtype, out_dtype, path, tiles, ds->cu_count,
+                   ds->occ[in_dtype][out_dtype], &pl);
+    if (rc) return rc;
+    g_plans.put(key, pl);
+  }
   const int64_t grid = pl.grid, need = pl.ws;
   const int chosen = pl.path;
   const VariantDesc& var = pl.v;

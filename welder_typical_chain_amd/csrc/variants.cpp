@@ -76,7 +76,7 @@ int in_class(int in_dt) {
 
 }  // namespace
 
-std::vector<VariantDesc> variants_for(int in_dt) {
+static std::vector<VariantDesc> make_variants(int in_dt) {
   std::vector<VariantDesc> v;
   if (!valid_in(in_dt)) return v;
   const int64_t tk = 128 / in_bytes(in_dt);
@@ -92,6 +92,13 @@ std::vector<VariantDesc> variants_for(int in_dt) {
     v.push_back({kVarRows, "rows128_wave64x32_k128", 128, 128, kRowsMaxK, 2, 16, 128, 1,
                  bit(WTC_PATH_ROWS)});
   return v;
+}
+
+const std::vector<VariantDesc>& variants_for(int in_dt) {
+  static const std::vector<VariantDesc> tables[5] = {
+      make_variants(WTC_DTYPE_F32), make_variants(WTC_DTYPE_F16), make_variants(WTC_DTYPE_BF16),
+      make_variants(WTC_DTYPE_FP8_E4M3), {}};
+  return tables[valid_in(in_dt) ? in_dt : 4];
 }
 
 bool find_variant(int in_dt, int64_t tm, int64_t tn, int64_t tk, int64_t ttm, int64_t ttn,
@@ -112,6 +119,24 @@ bool variant_by_id(int in_dt, int id, VariantDesc* out) {
       return true;
     }
   return false;
+}
+
+bool feasible(const VariantDesc& v, int path, const Problem& p) {
+  if (path < WTC_PATH_EXCHANGE || path > WTC_PATH_ROWS || !(v.paths & bit(path))) return false;
+  const int64_t nT = cdiv(p.n, 128);
+  switch (path) {
+    case WTC_PATH_EXCHANGE: {
+      const int64_t tiles = p.batch * cdiv(p.m, v.tile_rows) * nT;
+      return tiles <= (int64_t)p.cu_count * std::max(1, p.xch_per_cu) &&
+             nT <= kExchangeMaxColTiles && tiles <= kExchangeMaxTiles;
+    }
+    case WTC_PATH_SPLIT:
+      return nT <= kSplitMaxColTiles;
+    case WTC_PATH_ROWS:
+      return p.k <= kRowsMaxK;
+    default:
+      return true;
+  }
 }
 
 std::string infeasible_reason(const VariantDesc& v, int path, const Problem& p) {
@@ -207,13 +232,30 @@ std::vector<Choice> rank_choices(const Problem& p, int path, int variant) {
     if (variant >= 0 && v.id != variant) continue;
     for (int q = WTC_PATH_EXCHANGE; q <= WTC_PATH_ROWS; ++q) {
       if (path == WTC_PATH_AUTO ? q == WTC_PATH_UNFUSED : q != path) continue;
-      if (!infeasible_reason(v, q, p).empty()) continue;
+      if (!feasible(v, q, p)) continue;
       out.push_back({v, q, estimate_us(v, q, p)});
     }
   }
   std::stable_sort(out.begin(), out.end(),
                    [](const Choice& a, const Choice& b) { return a.est_us < b.est_us; });
   return out;
+}
+
+bool best_choice(const Problem& p, int path, int variant, Choice* out) {
+  bool found = false;
+  for (const VariantDesc& v : variants_for(p.in_dt)) {
+    if (variant >= 0 && v.id != variant) continue;
+    for (int q = WTC_PATH_EXCHANGE; q <= WTC_PATH_ROWS; ++q) {
+      if (path == WTC_PATH_AUTO ? q == WTC_PATH_UNFUSED : q != path) continue;
+      if (!feasible(v, q, p)) continue;
+      const double est = estimate_us(v, q, p);
+      if (!found || est < out->est_us) {  // ties keep the earlier pair, as the stable sort does
+        *out = Choice{v, q, est};
+        found = true;
+      }
+    }
+  }
+  return found;
 }
 
 }  // namespace wtc

@@ -40,8 +40,9 @@ struct VariantDesc {
   unsigned paths;  // bit (1 << WTC_PATH_x) for each path the variant runs
 };
 
-// The variants implemented for an input type (WTC_DTYPE_*), in id order.
-std::vector<VariantDesc> variants_for(int in_dt);
+// The variants implemented for an input type (WTC_DTYPE_*), in id order
+// (a static table: empty for an unknown type).
+const std::vector<VariantDesc>& variants_for(int in_dt);
 // The variant with exactly these five tile parameters, if any.
 bool find_variant(int in_dt, int64_t tile_m, int64_t tile_n, int64_t tile_k, int64_t thread_tile_m,
                   int64_t thread_tile_n, VariantDesc* out);
@@ -62,7 +63,9 @@ struct Problem {
   int xch_per_cu; // exchange-kernel workgroups one CU holds (1 with its LDS pad)
 };
 
-// Why a (variant, path) pair cannot run a problem; empty when it can.
+// Whether a (variant, path) pair can run a problem, and why not (empty when
+// it can; builds the message, so only for error reports).
+bool feasible(const VariantDesc& v, int path, const Problem& p);
 std::string infeasible_reason(const VariantDesc& v, int path, const Problem& p);
 
 // Estimated microseconds per back-to-back call of `path` on variant `v`.
@@ -77,6 +80,9 @@ struct Choice {
 // ranks the fused paths (exchange, split, rows); another path ranks only that
 // one; `variant` >= 0 keeps only that variant.
 std::vector<Choice> rank_choices(const Problem& p, int path, int variant = -1);
+// The first of rank_choices without building the list; false when nothing
+// is feasible.
+bool best_choice(const Problem& p, int path, int variant, Choice* out);
 
 // Grid of the path's first kernel.
 int64_t variant_grid(const VariantDesc& v, int path, const Problem& p);
