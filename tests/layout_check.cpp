@@ -1,4 +1,5 @@
-// layout_check.cpp -- CPU replay of one workgroup of chain_tile_kernel.
+// layout_check.cpp -- CPU replay of one workgroup of chain_tile_kernel (and
+// of one k-slab of chain_wide_kernel's 256x256 tile).
 //
 // Uses the kernel's own index maps (welder_typical_chain_amd/csrc/tile_layout.h)
 // to move one k-tile of A and B from "HBM" through the register transpose into
@@ -321,9 +322,131 @@ static void run_dma8() {
   CHECK(cr.worst == 1, "[dma8] tr8 reads conflict\n");
 }
 
+// The 256x256 tile of wide_tile.hip: one 64-byte k-slab of A (256 rows,
+// a64 layout) and B (two 128-column halves in the K-major layouts) staged by
+// the 4 waves' direct-to-LDS loads (wave w: A blocks 4w..4w+3, B blocks
+// 4(w%2)..+3 of half w/2), then every wave's fragment reads from the kernel's
+// per-lane bases plus compile-time offsets, checked against the operands
+// the MFMA must see (A row / B column of the lane, the same k on both).
+static void run_wide(int sz) {
+  const char* name = sz == 1 ? "wide8" : "wide16";
+  const int KE = 64 / sz;       // k per slab
+  const int EPC = 16 / sz;      // elements per chunk
+  const int TM = 256, TN = 256;
+  std::vector<uint8_t> A((size_t)TM * KE * sz), B((size_t)KE * TN * sz);
+  for (size_t i = 0; i < A.size(); ++i) A[i] = (uint8_t)((i * 7 + 3) % 251);
+  for (size_t i = 0; i < B.size(); ++i) B[i] = (uint8_t)((i * 13 + 5) % 241);
+  auto a_at = [&](int m, int k, int byte) { return A[((size_t)m * KE + k) * sz + byte]; };
+  auto b_at = [&](int k, int n, int byte) { return B[((size_t)k * TN + n) * sz + byte]; };
+  const int ASTAGE = TM * 64, BHALF = 8192;
+  std::vector<uint8_t> st(ASTAGE + 2 * BHALF);
+  std::vector<int> cov(st.size(), 0);
+  for (int w = 0; w < 4; ++w)
+    for (int q = 0; q < 4; ++q)
+      for (int i = 0; i < 64; ++i) {
+        // A block 4w + q
+        const int ba = 4 * w + q;
+        const int row = dma64_a_row(ba, i), c = dma64_a_chunk(ba, i);
+        CHECK(row == dma64_a_row(4 * w, i) + 16 * q && c == dma64_a_chunk(0, i),
+              "[%s] A block step (wave %d q %d lane %d)\n", name, w, q, i);
+        const int dst = ba * 1024 + 16 * i;
+        CHECK(a64_lds_offset(row, c) == dst, "[%s] A lane %d of block %d lands off-layout\n", name, i, ba);
+        for (int x = 0; x < 16; ++x) {
+          st[dst + x] = A[(size_t)row * KE * sz + c * 16 + x];
+          cov[dst + x]++;
+        }
+        // B block 4(w%2) + q of half w/2
+        const int half = w >> 1, bb = 4 * (w & 1) + q;
+        const int kr = sz == 1 ? dma8_b_row(bb, i) : dma_b_row(bb, i);
+        const int cc = sz == 1 ? dma8_b_chunk(bb, i) : dma_b_chunk(bb, i);
+        const int bdst = bb * 1024 + 16 * i;
+        CHECK((sz == 1 ? btr8_offset(kr, 16 * cc) : btr_offset(kr, 8 * cc)) == bdst,
+              "[%s] B lane %d of block %d lands off-layout\n", name, i, bb);
+        CHECK(kr < KE, "[%s] B k-row %d past the slab\n", name, kr);
+        const int n0 = 128 * half + EPC * cc;
+        for (int x = 0; x < 16; ++x) {
+          st[ASTAGE + half * BHALF + bdst + x] = b_at(kr, n0 + x / sz, x % sz);
+          cov[ASTAGE + half * BHALF + bdst + x]++;
+        }
+      }
+  for (size_t i = 0; i < cov.size(); ++i) CHECK(cov[i] == 1, "[%s] LDS byte %zu written %d times\n", name, i, cov[i]);
+  Conflicts ca, cb;
+  for (int wave = 0; wave < 4; ++wave) {
+    const int wm = wave >> 1, wn = wave & 1;
+    for (int s = 0; s < (sz == 1 ? 1 : 2); ++s)
+      for (int mt = 0; mt < 4; ++mt)
+        for (int nt = 0; nt < 4; ++nt) {
+          // per lane: the operand bytes of MFMA (s, mt, nt), assembled as the kernel does
+          std::vector<int> a_addr[2], b_addr[4];
+          for (int l = 0; l < 64; ++l) {
+            const int r = frag_row(l);
+            const int row = wm * 128 + mt * 32 + r, col = wn * 128 + nt * 32 + r;
+            uint8_t aop[32], bop[32];
+            const int nbytes = sz == 1 ? 32 : 16;  // operand bytes per lane
+            for (int hh = 0; hh < (sz == 1 ? 2 : 1); ++hh) {
+              const int chunk = sz == 1 ? frag64_chunk8(l, hh) : frag64_chunk16(l, s);
+              const int base = a64_lds_offset(wm * 128 + r, chunk);
+              CHECK(a64_lds_offset(row, chunk) == base + mt * 2048, "[%s] A base + 2048*mt (lane %d)\n", name, l);
+              std::memcpy(&aop[16 * hh], &st[base + mt * 2048], 16);
+              a_addr[hh].push_back(base + mt * 2048);
+            }
+            for (int e = 0; e < nbytes; ++e) {
+              const int kk = sz == 1 ? 32 * (l >> 5) + e : 16 * s + 8 * (l >> 5) + e / 2;
+              CHECK(aop[e] == a_at(row, kk, e % sz), "[%s] A operand wave %d lane %d byte %d\n", name, wave, l, e);
+            }
+            (void)bop;
+            (void)col;
+          }
+          // B: the transpose reads of n-subtile nt (lanes exchange within groups of 16)
+          const int qn = sz == 1 ? 4 : 2;
+          std::vector<std::vector<uint8_t>> src(qn, std::vector<uint8_t>(64 * 8));
+          for (int q = 0; q < qn; ++q)
+            for (int l = 0; l < 64; ++l) {
+              const int base = wn * BHALF + (sz == 1 ? btr8_offset(btr8_k(0, 0, l), btr8_n(nt * 32, l))
+                                                     : btr_offset(btr_k(0, 0, l), btr_n(nt * 32, l)));
+              const int off = base + (sz == 1 ? 8 * q * 128 : (16 * s + 4 * q) * 256);
+              const int ref = wn * BHALF + (sz == 1 ? btr8_offset(btr8_k(0, q, l), btr8_n(nt * 32, l))
+                                                    : btr_offset(btr_k(s, q, l), btr_n(nt * 32, l)));
+              CHECK(off == ref, "[%s] B base + k-rows (lane %d q %d)\n", name, l, q);
+              std::memcpy(&src[q][8 * l], &st[ASTAGE + off], 8);
+              b_addr[q].push_back(ASTAGE + off);
+            }
+          for (int l = 0; l < 64; ++l) {
+            const int col = wn * 128 + nt * 32 + (l & 31);
+            for (int q = 0; q < qn; ++q)
+              for (int r = 0; r < (sz == 1 ? 8 : 4); ++r) {
+                uint8_t got[2];
+                int kk;
+                if (sz == 1) {  // byte r of lane l: byte l%8 of lane 2r + (l%16)/8 of its group
+                  got[0] = src[q][8 * (16 * (l / 16) + 2 * r + (l % 16) / 8) + (l % 16) % 8];
+                  kk = 32 * (l >> 5) + 8 * q + r;
+                } else {  // element r of lane l: element l%4 of lane 4r + (l%16)/4 of its group
+                  const int sl = 16 * (l / 16) + 4 * r + (l % 16) / 4;
+                  std::memcpy(got, &src[q][8 * sl + 2 * ((l % 16) % 4)], 2);
+                  kk = 16 * s + 8 * (l >> 5) + 4 * q + r;
+                }
+                for (int byte = 0; byte < sz; ++byte)
+                  CHECK(got[byte] == b_at(kk, col, byte), "[%s] B operand wave %d lane %d q %d r %d\n", name, wave,
+                        l, q, r);
+              }
+          }
+          for (int hh = 0; hh < 2; ++hh)
+            for (size_t p0 = 0; p0 < a_addr[hh].size(); p0 += 16)
+              ca.phase(std::vector<int>(a_addr[hh].begin() + p0, a_addr[hh].begin() + p0 + 16), 16);
+          for (int q = 0; q < qn; ++q)
+            for (size_t p0 = 0; p0 < 64; p0 += 32)
+              cb.phase(std::vector<int>(b_addr[q].begin() + p0, b_addr[q].begin() + p0 + 32), 8);
+        }
+  }
+  std::printf("[%s] A-read / B-read bank-conflict ways: %d / %d\n", name, ca.worst, cb.worst);
+  CHECK(ca.worst == 1 && cb.worst == 1, "[%s] fragment reads conflict\n", name);
+}
+
 int main() {
   run_dma16();
   run_dma8();
+  run_wide(2);
+  run_wide(1);
   run(2, "f16/bf16");
   run(1, "fp8");
   run(4, "f32");

@@ -73,17 +73,18 @@ def test_plan_headline_and_configs(L):
     rc, grid, path, _ = plan(L, 64, 2048, 2048, 128, 1, 1, _lib.PATH_AUTO)
     assert (rc, grid, path) == (0, 64 * 16, _lib.PATH_ROWS)
     rc, grid, path, _ = plan(L, 64, 2048, 2048, 128, 1, 1, _lib.PATH_SPLIT)
-    assert (rc, grid, path) == (0, 64 * 8 * 16, _lib.PATH_SPLIT)  # 256-row tiles
+    assert (rc, grid, path) == (0, 64 * 8 * 8, _lib.PATH_SPLIT)  # 256x256 tiles
     # the rows path needs 16-bit inputs and k <= 128
     assert plan(L, 64, 2048, 2048, 256, 1, 1, _lib.PATH_AUTO)[2] == _lib.PATH_SPLIT
     assert plan(L, 64, 2048, 2048, 128, _lib.DTYPE_FP8_E4M3, 1, _lib.PATH_AUTO)[2] == _lib.PATH_SPLIT
     rc, *_ = plan(L, 1, 256, 256, 256, 1, 1, _lib.PATH_ROWS)
     assert rc == _lib.WTC_ERR_UNSUPPORTED and b"rows path" in L.wtc_last_error()
-    # C4: 256 column tiles per row -> split, with 256-row tiles (4 x 256)
+    # C4: 256 column tiles per row -> split, with 256x256 tiles (4 x 128)
     rc, grid, path, _ = plan(L, 1, 1024, 32768, 4096, _lib.DTYPE_BF16, 1, _lib.PATH_AUTO)
-    assert (rc, grid, path) == (0, 4 * 256, _lib.PATH_SPLIT)
-    # C5 (fp8): split (128-row k-split tiles measure within 1.3 % of 256-row ones)
-    assert plan(L, 1, 8192, 8192, 4096, _lib.DTYPE_FP8_E4M3, 1, _lib.PATH_AUTO)[2] == _lib.PATH_SPLIT
+    assert (rc, grid, path) == (0, 4 * 128, _lib.PATH_SPLIT)
+    # C5 (fp8): split, 256x256 tiles (32 x 32)
+    rc, grid, path, _ = plan(L, 1, 8192, 8192, 4096, _lib.DTYPE_FP8_E4M3, 1, _lib.PATH_AUTO)
+    assert (rc, grid, path) == (0, 32 * 32, _lib.PATH_SPLIT)
     # f32 has one layout (128-row tiles)
     assert plan(L, 1, 1024, 32768, 64, _lib.DTYPE_F32, 0, _lib.PATH_SPLIT)[1] == 8 * 256
     # forcing the exchange path where it cannot be co-resident is refused
@@ -101,22 +102,23 @@ F16, BF16, FP8, F32 = _lib.DTYPE_F16, _lib.DTYPE_BF16, _lib.DTYPE_FP8_E4M3, _lib
 T128 = {F16: [128, 128, 64, 2, 16], BF16: [128, 128, 64, 2, 16], FP8: [128, 128, 128, 2, 16]}
 KS2 = {F16: [128, 128, 64, 2, 32], BF16: [128, 128, 64, 2, 32], FP8: [128, 128, 128, 2, 32]}
 T256 = {F16: [256, 128, 64, 2, 32], BF16: [256, 128, 64, 2, 32], FP8: [256, 128, 128, 2, 32]}
+W256 = {F16: [256, 256, 32, 4, 64], BF16: [256, 256, 32, 4, 64], FP8: [256, 256, 64, 4, 64]}
 ROWS = [128, 128, 128, 2, 16]
 
 
 def test_variant_table(L):
-    """Four variants for 16-bit inputs, three for fp8 (no rows kernel), one
-    for f32; tiles distinct within an input type; each runs the paths its
-    kernels implement."""
+    """Five variants for 16-bit inputs, four for fp8 (no rows kernel), one
+    for f32, in id order; tiles distinct within an input type; each runs the
+    paths its kernels implement."""
     ex, sp, un, ro = (1 << _lib.PATH_EXCHANGE, 1 << _lib.PATH_SPLIT, 1 << _lib.PATH_UNFUSED,
                       1 << _lib.PATH_ROWS)
     for dt in (F16, BF16):
         vs = _lib.variants(dt)
-        assert [v[1] for v in vs] == [T128[dt], KS2[dt], T256[dt], ROWS]
-        assert [v[2] for v in vs] == [ex | sp | un, ex | sp | un, sp | un, ro]
-    assert [v[1] for v in _lib.variants(FP8)] == [T128[FP8], KS2[FP8], T256[FP8]]
+        assert [v[1] for v in vs] == [T128[dt], KS2[dt], T256[dt], ROWS, W256[dt]]
+        assert [v[2] for v in vs] == [ex | sp | un, ex | sp | un, sp | un, ro, sp | un]
+    assert [v[1] for v in _lib.variants(FP8)] == [T128[FP8], KS2[FP8], T256[FP8], W256[FP8]]
     assert [v[1] for v in _lib.variants(F32)] == [[128, 128, 32, 2, 32]]
-    assert len({v[0] for dt in (F16, FP8, F32) for v in _lib.variants(dt)}) == 5
+    assert len({v[0] for dt in (F16, FP8, F32) for v in _lib.variants(dt)}) == 6
     assert L.wtc_list_variants(9, None, None, None, 0) == -1
 
 
@@ -124,17 +126,19 @@ def test_variant_table(L):
 # where the cost model picks the measured fastest (variant, path) on MI355X
 # (back-to-back calls); tests/test_cost_model.py scores every shape.
 MEASURED_BEST = [
-    ((1, 2048, 2048, 1024, F16, F16), KS2[F16], _lib.PATH_EXCHANGE),   # C2: 15.8 vs 16.3 us
+    ((1, 2048, 2048, 1024, F16, F16), KS2[F16], _lib.PATH_EXCHANGE),   # C2: 15.5 vs 15.8 us
     ((1, 2048, 2048, 64, F16, F16), T128[F16], _lib.PATH_EXCHANGE),    # 8.1 vs 8.9
-    ((1, 2048, 2048, 256, F16, F16), T128[F16], _lib.PATH_EXCHANGE),   # 9.7 vs 9.9
-    ((1, 8192, 128, 64, F16, F16), T128[F16], _lib.PATH_EXCHANGE),     # 5.6 vs rows 7.2
-    ((1, 4096, 4096, 1024, F16, F16), T256[F16], _lib.PATH_SPLIT),     # 64.9 vs 73.6
-    ((1, 2048, 8192, 512, F16, F16), T256[F16], _lib.PATH_SPLIT),      # 52.6 vs 65.0
-    ((8, 2048, 2048, 128, F16, F16), ROWS, _lib.PATH_ROWS),            # 50.2 vs split 57.1
-    ((16, 512, 512, 64, F16, F16), T128[F16], _lib.PATH_EXCHANGE),     # 7.6 vs rows 15.8
-    ((1, 4096, 2048, 128, F16, F16), T256[F16], _lib.PATH_SPLIT),      # 22.2 vs rows 49.0
-    ((64, 2048, 2048, 128, F16, F16), ROWS, _lib.PATH_ROWS),           # C3: 257 vs 497
-    ((1, 1024, 32768, 4096, BF16, BF16), T256[BF16], _lib.PATH_SPLIT),  # C4: 296 vs 352
+    ((1, 2048, 2048, 256, F16, F16), T128[F16], _lib.PATH_EXCHANGE),   # 9.6 vs 9.7
+    ((1, 8192, 128, 64, F16, F16), T128[F16], _lib.PATH_EXCHANGE),     # 5.6 vs 6.1
+    ((1, 4096, 4096, 1024, F16, F16), W256[F16], _lib.PATH_SPLIT),     # 53.3 vs 64.3
+    ((1, 2048, 8192, 512, F16, F16), W256[F16], _lib.PATH_SPLIT),      # 41.2 vs 52.0
+    ((8, 2048, 2048, 128, F16, F16), ROWS, _lib.PATH_ROWS),            # 50.0 vs split 56.9
+    ((16, 512, 512, 64, F16, F16), T128[F16], _lib.PATH_EXCHANGE),     # 7.6 vs 8.2
+    ((1, 4096, 2048, 128, F16, F16), T256[F16], _lib.PATH_SPLIT),      # 22.2 vs 24.6
+    ((1, 640, 8192, 4096, F16, F16), T256[F16], _lib.PATH_SPLIT),      # 62.5 vs 69.8 (96 wide tiles: 84.7)
+    ((64, 2048, 2048, 128, F16, F16), ROWS, _lib.PATH_ROWS),           # C3: 253 vs 476
+    ((1, 1024, 32768, 4096, BF16, BF16), W256[BF16], _lib.PATH_SPLIT),  # C4: 257 vs 292
+    ((1, 8192, 8192, 4096, FP8, F16), W256[FP8], _lib.PATH_SPLIT),     # C5: 260 vs 347
 ]
 
 
@@ -234,7 +238,7 @@ def compile_chain(L, path: Path, out: Path, tiles, fused=1, errsize=4096):
 
 EXPECT = {  # config -> (tiles of the variant the solver ranks first, its path)
     "C1": ([128, 128, 32, 2, 32], "exchange"), "C2": (KS2[F16], "exchange"), "C3": (ROWS, "rows"),
-    "C4": (T256[BF16], "split"), "C5": (KS2[FP8], "split"),
+    "C4": (W256[BF16], "split"), "C5": (W256[FP8], "split"),
 }
 
 
@@ -274,9 +278,10 @@ def test_solver_and_compile_per_config(L, tmp_path, name, named):
     assert launch["runtime_scales"] == (cfg.in_dtype == "fp8")
     assert abs(launch["logit_scale"] - cfg.logit_scale) < 1e-6
     plan_json = json.loads((out / "04.kernel.plan.json").read_text())
-    assert plan_json["kernels"][0]["name"].startswith("chain_rows_kernel" if path == "rows"
-                                                      else "chain_tile_kernel")
-    assert plan_json["kernels"][0]["block"][0] == (256 if cfg.in_dtype == "f32" else 512)
+    wide = tiles[:2] == [256, 256]
+    assert plan_json["kernels"][0]["name"].startswith(
+        "chain_rows_kernel" if path == "rows" else ("chain_wide_kernel" if wide else "chain_tile_kernel"))
+    assert plan_json["kernels"][0]["block"][0] == (256 if cfg.in_dtype == "f32" or wide else 512)
     report = dict(l.split("=", 1) for l in (out / "kernel_report.txt").read_text().splitlines()
                   if "=" in l and " " not in l.split("=", 1)[0])
     assert int(report["launch_kernel_count"]) == (2 if path == "split" else 1)

@@ -44,7 +44,8 @@ LLVM_BIN = Path(os.environ.get("ROCM_PATH", "/opt/rocm")) / "llvm" / "bin"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
-HIP_SOURCES = ["fused_matmul_softmax.hip", "rowblock_softmax.hip", "unfused_chain.hip", "launch.hip"]
+HIP_SOURCES = ["fused_matmul_softmax.hip", "wide_tile.hip", "rowblock_softmax.hip", "unfused_chain.hip",
+               "launch.hip"]
 CXX_SOURCES = ["chain_recognizer.cpp", "variants.cpp", "tile_solver.cpp", "compile_capi.cpp"]
 
 HIP_FLAGS = [
@@ -58,9 +59,10 @@ HIP_FLAGS = [
     f"-I{ROOT / 'include'}",
     f"-I{CSRC}",
 ]
-# Per-source extra flags.  The chain tile kernel takes its first-load scalars
-# as leading arguments; gfx950 preloads those into SGPRs.
-HIP_EXTRA = {"fused_matmul_softmax.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"]}
+# Per-source extra flags.  The tile kernels take their first-load scalars as
+# leading arguments; gfx950 preloads those into SGPRs.
+HIP_EXTRA = {"fused_matmul_softmax.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"],
+             "wide_tile.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"]}
 CXX_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra",
              f"-I{ROOT / 'include'}", f"-I{CSRC}"]
 

@@ -183,13 +183,15 @@ def time_case(shape, tiles, path, device, target_ms=20.0):
 
 _VARIANT_IDS = {"tile128x128_wave64x32": 0, "tile128x128_wave64x64": 0,
                 "tile128x128_wave64x64_ksplit2": 1, "tile256x128_wave64x64": 2,
-                "rows128_wave64x32_k128": 3}
+                "rows128_wave64x32_k128": 3, "tile256x256_wave128x128": 4}
+# tile rows and columns per tile variant id
+_TILE = {0: (128, 128), 1: (128, 128), 2: (256, 128), 4: (256, 256)}
 _IN_BYTES = {"f32": 4, "f16": 2, "bf16": 2, "fp8": 1}
 _OUT_BYTES = {"f32": 4, "f16": 2, "bf16": 2}
 # own k-tile cycles per (variant, input class 0 16-bit / 1 fp8 / 2 f32),
 # fixed cycles per (variant, epilogue 0 exchange / 1 split), then scalars
-_KT = [(0, 0), (0, 1), (0, 2), (1, 0), (1, 1), (2, 0), (2, 1)]
-_FX = [(0, 0), (0, 1), (1, 0), (1, 1), (2, 1)]
+_KT = [(0, 0), (0, 1), (0, 2), (1, 0), (1, 1), (2, 0), (2, 1), (4, 0), (4, 1)]
+_FX = [(0, 0), (0, 1), (1, 0), (1, 1), (2, 1), (4, 1)]
 _SCALARS = ["launch_us", "exchange_us", "exchange_per_tile_us", "hbm_gbs", "feed_gbs",
             "rows_block_cyc", "rows_tile_cyc", "rows_kstep_cyc"]
 
@@ -217,8 +219,9 @@ def model_us(x, r, cu=256):
         f = _clock_ghz(blocks / (waves * cu))
         cyc = c["rows_block_cyc"] + n_t * (c["rows_tile_cyc"] + c["rows_kstep_cyc"] * math.ceil(k / 16))
         return c["launch_us"] + max(waves * cyc / (f * 1e3), (ab + elems * osz) * us_per_byte)
-    rows = 256 if v == 2 else 128
+    rows, cols = _TILE[v]
     cls = 1 if r["in"] == "fp8" else (2 if r["in"] == "f32" else 0)
+    n_t = math.ceil(n / cols)
     tiles = b * math.ceil(m / rows) * n_t
     waves = math.ceil(tiles / cu)
     f = _clock_ghz(tiles / (waves * cu))
@@ -228,7 +231,7 @@ def model_us(x, r, cu=256):
     t_tiles = 0.0
     for count, active in ((full, cu), (1 if rem else 0, rem)):
         if count:
-            per_kt = kt[(v, cls)] + (rows + 128) * 128 * active * f / c["feed_gbs"]
+            per_kt = kt[(v, cls)] + (rows + cols) * 128 * active * f / c["feed_gbs"]
             t_tiles += count * (fx[(v, epi)] + nk * per_kt) / (f * 1e3)
     if r["path"] == "exchange":
         t_xch = c["exchange_us"] + c["exchange_per_tile_us"] * n_t if n > 128 else 0.0

@@ -12,6 +12,7 @@
 #include <filesystem>
 #include <map>
 #include <sstream>
+#include <utility>
 #include <vector>
 
 #include "chain_spec.h"
@@ -24,6 +25,7 @@ namespace wtc {
 // Workgroup sizes of the kernels (defined with the kernels and the launcher
 // in the library).
 int chain_kernel_threads(int in_dt);
+int wide_kernel_threads();
 int rows_kernel_threads();
 int rescale_waves_per_row(int64_t rows_total, int cu_count);
 // Compute units of the current device, or `fallback` when no GPU is visible.
@@ -185,28 +187,42 @@ static int compile_impl(const char* input_mlir_path, const char* out_dir, int64_
     return "_ZN3wtc17chain_tile_kernelILi" + std::to_string(in) + "ELi" + std::to_string(out) +
            "ELi" + std::to_string(epi) + "ELi3ELi" + std::to_string(tm) + "ELi" + std::to_string(ks) + "E";
   };
+  // chain_wide_kernel<in, out, epi>: the 256x256 tiles
+  auto wide_sym = [](int in, int out, int epi) {
+    return "_ZN3wtc17chain_wide_kernelILi" + std::to_string(in) + "ELi" + std::to_string(out) +
+           "ELi" + std::to_string(epi) + "E";
+  };
+  const bool wide = var.id == kVarTile256x256;
+  // the split / unfused tile kernel of the variant: display name and symbol
+  auto tile_kern = [&](int out, const std::string& out_name, int epi, const std::string& epi_name) {
+    if (wide) return std::make_pair("chain_wide_kernel<" + kin + "," + out_name + "," + epi_name + ",256x256>",
+                                    wide_sym(in_code, out, epi));
+    const std::string layout = std::to_string(var.tile_rows) + "x128" + (var.ks == 2 ? ",ksplit2" : "");
+    return std::make_pair("chain_tile_kernel<" + kin + "," + out_name + "," + epi_name + "," + layout + ">",
+                          chain_sym(in_code, out, epi, var.tile_rows, var.ks));
+  };
   const std::string out_t = "ILi" + std::to_string(out_code) + "E";
   std::vector<K> ks;
   const int64_t rows = spec.batch * spec.m;
-  const int tile_threads = chain_kernel_threads(in_code);
-  const std::string layout = std::to_string(var.tile_rows) + "x128" + (var.ks == 2 ? ",ksplit2" : "");
+  const int tile_threads = wide ? wide_kernel_threads() : chain_kernel_threads(in_code);
   if (path == WTC_PATH_ROWS) {
     ks.push_back({"chain_rows_kernel<" + kin + "," + kout + ">",
                   "_ZN3wtc17chain_rows_kernelILi" + std::to_string(in_code) + "ELi" +
                       std::to_string(out_code) + "E",
                   grid, 0, rows_kernel_threads()});
   } else if (path == WTC_PATH_EXCHANGE) {
-    ks.push_back({"chain_tile_kernel<" + kin + "," + kout + ",exchange," + layout + ">",
+    ks.push_back({"chain_tile_kernel<" + kin + "," + kout + ",exchange,128x128" +
+                      (var.ks == 2 ? ",ksplit2" : "") + ">",
                   chain_sym(in_code, out_code, 0, 128, var.ks), grid,
                   exchange_lds_pad(in_code, out_code, var.ks), tile_threads});
   } else if (path == WTC_PATH_SPLIT) {
-    ks.push_back({"chain_tile_kernel<" + kin + "," + kout + ",split," + layout + ">",
-                  chain_sym(in_code, out_code, 1, var.tile_rows, var.ks), grid, 0, tile_threads});
+    const auto tk = tile_kern(out_code, kout, 1, "split");
+    ks.push_back({tk.first, tk.second, grid, 0, tile_threads});
     ks.push_back({"rescale_rows_kernel<" + kout + ">", "_ZN3wtc19rescale_rows_kernel" + out_t,
                   (rows * rescale_waves_per_row(rows, cu_count) + 3) / 4, 0});
   } else {
-    ks.push_back({"chain_tile_kernel<" + kin + ",f32,logits," + layout + ">",
-                  chain_sym(in_code, 0, 2, var.tile_rows, var.ks), grid, 0, tile_threads});
+    const auto tk = tile_kern(0, "f32", 2, "logits");
+    ks.push_back({tk.first, tk.second, grid, 0, tile_threads});
     ks.push_back({"rowmax_kernel", "_ZN3wtc13rowmax_kernel", rows, 0});
     ks.push_back({"expsub_kernel", "_ZN3wtc13expsub_kernel", rows, 0});
     ks.push_back({"rowsum_kernel", "_ZN3wtc13rowsum_kernel", rows, 0});

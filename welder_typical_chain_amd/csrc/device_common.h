@@ -1,5 +1,5 @@
 // device_common.h -- device-side helpers shared by the gfx950 chain kernels
-// (fused_matmul_softmax.hip, rowblock_softmax.hip): vector types, buffer
+// (fused_matmul_softmax.hip, rowblock_softmax.hip, wide_tile.hip): vector types, buffer
 // descriptors and loads, direct-to-LDS loads with hand-counted waits, the
 // LDS transpose read, output packing and wave reductions.
 #pragma once
@@ -111,5 +111,12 @@ __device__ inline float dpp_quad(float x) {
 }
 __device__ inline float wave_xor32_sum(float x) { return x + __shfl_xor(x, 32); }
 
+// 64-bit relaxed atomic access at agent scope for the split path's per-tile
+// row statistics (max, sumexp): one store, so a reader never sees half of it.
+__device__ inline void store_stat(float2* p, float m, float s) {
+  const uint64_t u = (uint64_t)__builtin_bit_cast(uint32_t, m) |
+                     ((uint64_t)__builtin_bit_cast(uint32_t, s) << 32);
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 }  // namespace wtc

@@ -510,19 +510,6 @@ __device__ inline void mma_piece8(const KTileFrags8<NTN, KSW>& f, int i, f32x16 
   acc[mt][nt] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bv, av, acc[mt][nt], 0, 0, 0, 0, 0, 0);
 }
 
-// 64-bit relaxed atomic access at agent scope for the row statistics.
-__device__ inline void store_stat(float2* p, float m, float s) {
-  const uint64_t u = (uint64_t)__builtin_bit_cast(uint32_t, m) |
-                     ((uint64_t)__builtin_bit_cast(uint32_t, s) << 32);
-  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ inline float2 load_stat(const float2* p) {
-  const uint64_t u = __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-  const uint32_t lo = (uint32_t)u, hi = (uint32_t)(u >> 32);
-  return make_float2(__builtin_bit_cast(float, lo), __builtin_bit_cast(float, hi));
-}
-
 // ---- row exchange of the exchange path --------------------------------------
 // The tiles of a row block (all co-resident) exchange per-row log-sum-exps
 // through tagged entries instead of a barrier.  Tile (row block rbg, column
@@ -1090,7 +1077,8 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
 }
 
 // -------------------------------------------------------------------------
-// Second pass of the split (online two-pass) softmax.  `wpr` waves share a
+// Second pass of the split (online two-pass) softmax over tiles of
+// 2^tshift columns (128 or 256).  `wpr` waves share a
 // row (the launcher picks it so that few, wide rows still give every CU
 // enough waves); wave `part` of a row takes its 16-byte chunks part, part +
 // wpr, ... in steps of 64 lanes.  Every wave merges the row's nT tile
@@ -1103,7 +1091,7 @@ template <int OUT_DT>
 __global__ void __launch_bounds__(256)
 rescale_rows_kernel(uint8_t* __restrict__ out, const float2* __restrict__ partial,
                     int64_t rows_total, int64_t M, int64_t rows_pad, int64_t N,
-                    int64_t ldo_bytes, int64_t o_bstride, int nT, int wpr) {
+                    int64_t ldo_bytes, int64_t o_bstride, int nT, int tshift, int wpr) {
   constexpr int MAX_NT = 512;
   constexpr int U = 4;  // chunks in flight per lane
   __shared__ float fac[4][MAX_NT];
@@ -1168,12 +1156,12 @@ rescale_rows_kernel(uint8_t* __restrict__ out, const float2* __restrict__ partia
 #pragma unroll
     for (int i = 0; i < U; ++i) {
       const int64_t n = (c + i * step) * EPC;
-      *reinterpret_cast<u32x4*>(rowp + (c + i * step) * 16) = scale(v[i], fac[w][n / BN]);
+      *reinterpret_cast<u32x4*>(rowp + (c + i * step) * 16) = scale(v[i], fac[w][n >> tshift]);
     }
   }
   for (; c < nch; c += step) {
     const int64_t n = c * EPC;
-    *reinterpret_cast<u32x4*>(rowp + c * 16) = scale(*reinterpret_cast<const u32x4*>(rowp + c * 16), fac[w][n / BN]);
+    *reinterpret_cast<u32x4*>(rowp + c * 16) = scale(*reinterpret_cast<const u32x4*>(rowp + c * 16), fac[w][n >> tshift]);
   }
 }
 

@@ -380,6 +380,17 @@ int launch_chain(const void* kern, int threads, int64_t grid, int lds_dyn,
   return WTC_OK;
 }
 
+// The tile kernel of a variant for an epilogue (NULL when not built), and
+// its workgroup size.
+struct TileKernel {
+  const void* fn;
+  int threads;
+};
+TileKernel tile_kernel(const VariantDesc& v, int in_dt, int out_dt, int epi) {
+  if (v.id == kVarTile256x256) return {wide_kernel_symbol(in_dt, out_dt, epi), wide_kernel_threads()};
+  return {chain_kernel_symbol(in_dt, out_dt, epi, v.tile_rows, v.ks), chain_kernel_threads(in_dt)};
+}
+
 // chain_tile_kernel: the scalars a tile needs before its first load lead the
 // argument list (preloaded into SGPRs), then the parameter block.  check_args
 // keeps every batch slice below 2 GiB, so the 32-bit sizes and strides hold.
@@ -796,7 +807,8 @@ int matmul_softmax_impl(const void* a, const void* b, void* out, int64_t batch, 
   // row blocks per batch of the kernel that runs
   const int tile_rows = var.tile_rows;
   p.nRB = (int)ceil_div(m, tile_rows);
-  p.nT = (int)ceil_div(n, kTile);
+  // column tiles per row block: the variant's on the split and unfused paths
+  p.nT = (int)ceil_div(n, chosen == WTC_PATH_SPLIT || chosen == WTC_PATH_UNFUSED ? var.tile_n : kTile);
   p.partial = reinterpret_cast<float2*>(wsb + L.stats_off);
   p.ent = reinterpret_cast<uint64_t*>(wsb + L.stats_off);
   p.gen = reinterpret_cast<uint32_t*>(wsb + L.gen_off);
@@ -813,8 +825,8 @@ int matmul_softmax_impl(const void* a, const void* b, void* out, int64_t batch, 
                            chain_kernel_threads(in_dtype), grid,
                            exchange_lds_pad(in_dtype, out_dtype, var.ks), p, stream);
   if (chosen == WTC_PATH_SPLIT) {
-    rc = launch_tile(chain_kernel_symbol(in_dtype, out_dtype, kEpiSplit, tile_rows, var.ks),
-                     chain_kernel_threads(in_dtype), grid, 0, p, stream);
+    const TileKernel tk = tile_kernel(var, in_dtype, out_dtype, kEpiSplit);
+    rc = launch_tile(tk.fn, tk.threads, grid, 0, p, stream);
     if (rc) return rc;
     uint8_t* o = p.out;
     const float2* part = p.partial;
@@ -822,8 +834,9 @@ int matmul_softmax_impl(const void* a, const void* b, void* out, int64_t batch, 
     int64_t rows_total = batch * m, M_ = m, rows_pad = (int64_t)p.nRB * tile_rows, N_ = n,
             ldo = p.ldo_bytes, ob = p.o_bstride;
     int nT = p.nT;
+    int tshift = var.tile_n == 256 ? 8 : 7;  // log2 of the tile width
     int wpr = rescale_waves_per_row(rows_total, ds->cu_count);
-    void* args[] = {&o, &part, &rows_total, &M_, &rows_pad, &N_, &ldo, &ob, &nT, &wpr};
+    void* args[] = {&o, &part, &rows_total, &M_, &rows_pad, &N_, &ldo, &ob, &nT, &tshift, &wpr};
     HIP_TRY(hipLaunchKernel(rescale_kernel_symbol(out_dtype),
                             dim3((unsigned)ceil_div(rows_total * wpr, kRescaleRowsPerWg)), dim3(256),
                             args, 0, stream));
@@ -837,8 +850,8 @@ int matmul_softmax_impl(const void* a, const void* b, void* out, int64_t batch, 
   q.out = reinterpret_cast<uint8_t*>(logits);
   q.o_bstride = m * n * 4;
   q.ldo_bytes = n * 4;
-  rc = launch_tile(chain_kernel_symbol(in_dtype, DT_F32, kEpiLogits, tile_rows, var.ks),
-                   chain_kernel_threads(in_dtype), grid, 0, q, stream);
+  const TileKernel tk = tile_kernel(var, in_dtype, DT_F32, kEpiLogits);
+  rc = launch_tile(tk.fn, tk.threads, grid, 0, q, stream);
   if (rc) return rc;
   const int64_t rows = batch * m;
   if (rows > 0x7FFFFFFFll) return fail(WTC_ERR_UNSUPPORTED, "too many rows");

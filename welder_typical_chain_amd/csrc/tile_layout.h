@@ -169,6 +169,29 @@ WTC_HD constexpr int btr8_k(int s, int q, int lane) {
 }
 WTC_HD constexpr int btr8_n(int nb, int lane) { return nb + 16 * ((lane >> 4) & 1) + 8 * (lane & 1); }
 
+// ---- 64-byte k-slabs of the 256x256 tiles -----------------------------------
+// A 256x256 tile stages 64 bytes of K per ring stage (a k-slab: 32 f16/bf16
+// or 64 fp8 values): A [256 rows][4 chunks], chunk c of row m at slot
+// c ^ ((m >> 2) & 3).  The 16 lanes of a fragment read (16 consecutive rows,
+// one chunk) then hit 16 distinct 16-byte bank groups: row m sits at group
+// 4 * (m % 4) of its 256-byte line plus the slot, and the slot differs for
+// m, m + 4, m + 8, m + 12.  B keeps the K-major layouts above (btr_offset,
+// btr8_offset): each 128-column half of the tile is one such B buffer of
+// 32 (16-bit) or 64 (fp8) k-rows.
+WTC_HD constexpr int a64_lds_offset(int m, int c) { return m * 64 + ((c ^ ((m >> 2) & 3)) << 4); }
+// Direct-to-LDS block b of A (1 KiB) = rows 16b .. 16b+15; lane i lands in
+// row 16b + i/4, slot i%4, so it fetches chunk slot ^ ((row >> 2) & 3), which
+// does not depend on b.
+WTC_HD constexpr int dma64_a_row(int b, int lane) { return 16 * b + (lane >> 2); }
+WTC_HD constexpr int dma64_a_chunk(int b, int lane) {
+  return (lane & 3) ^ ((dma64_a_row(b, lane) >> 2) & 3);
+}
+// MFMA A fragments from a k-slab: 16-bit k-step s (0, 1) takes chunk
+// 2s + lane/32 of row lane%32; fp8 (one k-step of 64) takes chunks
+// 2*(lane/32) + hh, hh = 0, 1.
+WTC_HD constexpr int frag64_chunk16(int lane, int s) { return 2 * s + (lane >> 5); }
+WTC_HD constexpr int frag64_chunk8(int lane, int hh) { return 2 * (lane >> 5) + hh; }
+
 // ---- workgroup -> tile ------------------------------------------------------
 // Workgroups are dispatched round-robin over the 8 XCDs (blockIdx % 8).
 // tile_of_block() first gives XCD x the contiguous range of logical ids

@@ -28,39 +28,41 @@ constexpr unsigned kSplitPaths = bit(WTC_PATH_SPLIT) | bit(WTC_PATH_UNFUSED);
 // rescale; unfused: four f32 row passes), plus the row exchange (a fixed
 // part and a part per column tile of a row block).  The full waves (every
 // CU busy) and the last, partial one are priced separately.  One tile's
-// cycles are a fixed part (first loads and epilogue) and, per 128-byte
-// k-tile, the variant's own cycles plus the cycles its wave's A and B
-// k-tiles add as they stream in (bytes of every active tile over a
-// chip-wide rate).
+// cycles are a fixed part (first loads and epilogue) and, per 128 bytes of
+// K, the variant's own cycles plus the cycles its A and B bytes add as they
+// stream in (bytes of every active tile over a chip-wide rate).
 //
 // The constants were fitted (least squares on the log of the time) to
 // back-to-back timings of every variant on every path over the 60 shapes
 // of calibrate.py on MI355X.  Fitted on three of its four shape sets and
-// scored on the fourth, in turn, the fused ranking lost 1.3 % on average
+// scored on the fourth, in turn, the fused ranking lost 1.0 % on average
 // against the measured fastest choice (the hand-written rules it replaces:
 // 5.3 %).
 struct TileCal {
   double kt_cyc;        // own cycles per k-tile
   double fixed_cyc[3];  // per tile: exchange, split, logits epilogues
 };
-// [variant][0: 16-bit, 1: fp8, 2: f32]; fixed parts shared across input types
-const TileCal kTileCal[3][3] = {
-    /* kVarTile128 */ {{624, {3691, 5924, 500}}, {550, {3691, 5924, 500}}, {4471, {3691, 5924, 500}}},
-    /* kVarTile128KSplit */ {{557, {4566, 6902, 2261}}, {494, {4566, 6902, 2261}}, {0, {0, 0, 0}}},
-    /* kVarTile256 */ {{1088, {0, 10990, 1175}}, {1217, {0, 10990, 1175}}, {0, {0, 0, 0}}},
+// [tile variant][0: 16-bit, 1: fp8, 2: f32]; fixed parts shared across input
+// types.  Rows: kVarTile128, kVarTile128KSplit, kVarTile256, kVarTile256x256.
+const TileCal kTileCal[4][3] = {
+    /* kVarTile128 */ {{658.4, {3754.4, 6262.6, 0}}, {580.1, {3754.4, 6262.6, 0}}, {4474.7, {3754.4, 6262.6, 0}}},
+    /* kVarTile128KSplit */ {{585.5, {4463.6, 7198.8, 1021}}, {530.4, {4463.6, 7198.8, 1021}}, {0, {0, 0, 0}}},
+    /* kVarTile256 */ {{1133.0, {0, 11531.6, 0}}, {1266.8, {0, 11531.6, 0}}, {0, {0, 0, 0}}},
+    /* kVarTile256x256 */ {{1949.5, {0, 22141.6, 5456}}, {1605.2, {0, 22141.6, 5456}}, {0, {0, 0, 0}}},
 };
+int cal_row(int id) { return id == kVarTile256x256 ? 3 : id; }
 // Rows kernel, cycles per row block: a fixed part, and per 128-column tile
 // (both passes) a fixed part and a part per 16-wide k-step.
-constexpr double kRowsBlockCyc = 2124, kRowsTileCyc = 4879, kRowsKstepCyc = 113.4;
+constexpr double kRowsBlockCyc = 1877.4, kRowsTileCyc = 4930.0, kRowsKstepCyc = 106.01;
 // Back-to-back launch cost of one kernel (us); the row exchange after the
 // last tile of a row block: fixed (us) and per column tile (us); the HBM
 // rate of the fused paths' streaming passes and the chip-wide rate that
 // prices k-tile bytes (GB/s).
-constexpr double kLaunchUs = 3.720, kExchangeUs = 0.104, kExchangePerTileUs = 0.105;
-constexpr double kHbmGBs = 6976.0, kFeedGBs = 61113.0;
+constexpr double kLaunchUs = 3.728, kExchangeUs = 0.3430, kExchangePerTileUs = 0.07890;
+constexpr double kHbmGBs = 7621.5, kFeedGBs = 75041.4;
 // Unfused row passes (one 256-thread workgroup per row, eight per CU): HBM
 // rate, and the rate one workgroup streams its row at (GB/s).
-constexpr double kRowPassHbmGBs = 5167.0, kRowPassWgGBs = 5.52;
+constexpr double kRowPassHbmGBs = 5280.0, kRowPassWgGBs = 5.582;
 
 // Core clock under load, from the call's mean share of busy CUs: 1.5 GHz
 // with every CU busy throughout, ~2.1 with half of them or fewer (the chip's
@@ -91,6 +93,9 @@ static std::vector<VariantDesc> make_variants(int in_dt) {
   if (in_dt == WTC_DTYPE_F16 || in_dt == WTC_DTYPE_BF16)
     v.push_back({kVarRows, "rows128_wave64x32_k128", 128, 128, kRowsMaxK, 2, 16, 128, 1,
                  bit(WTC_PATH_ROWS)});
+  // tile_k: one 64-byte k-slab per ring stage
+  v.push_back({kVarTile256x256, "tile256x256_wave128x128", 256, 256, tk / 2, 4, 64, 256, 1,
+               kSplitPaths});
   return v;
 }
 
@@ -123,7 +128,7 @@ bool variant_by_id(int in_dt, int id, VariantDesc* out) {
 
 bool feasible(const VariantDesc& v, int path, const Problem& p) {
   if (path < WTC_PATH_EXCHANGE || path > WTC_PATH_ROWS || !(v.paths & bit(path))) return false;
-  const int64_t nT = cdiv(p.n, 128);
+  const int64_t nT = cdiv(p.n, v.tile_n);
   switch (path) {
     case WTC_PATH_EXCHANGE: {
       const int64_t tiles = p.batch * cdiv(p.m, v.tile_rows) * nT;
@@ -146,7 +151,7 @@ std::string infeasible_reason(const VariantDesc& v, int path, const Problem& p) 
     return path == WTC_PATH_ROWS ? "rows path needs 16-bit inputs and k <= 128"
                                  : std::string("variant ") + v.name + " does not run the " +
                                        kPathNames[path] + " path";
-  const int64_t nT = cdiv(p.n, 128);
+  const int64_t nT = cdiv(p.n, v.tile_n);
   switch (path) {
     case WTC_PATH_EXCHANGE: {
       const int64_t tiles = p.batch * cdiv(p.m, v.tile_rows) * nT;
@@ -160,7 +165,10 @@ std::string infeasible_reason(const VariantDesc& v, int path, const Problem& p) 
       return "";
     }
     case WTC_PATH_SPLIT:
-      return nT > kSplitMaxColTiles ? "split path supports n <= 65536" : "";
+      return nT > kSplitMaxColTiles
+                 ? "split path supports n <= " + std::to_string(kSplitMaxColTiles * v.tile_n) +
+                       " with " + std::to_string(v.tile_n) + "-column tiles"
+                 : "";
     case WTC_PATH_ROWS:
       return p.k > kRowsMaxK ? "rows path needs 16-bit inputs and k <= 128" : "";
     default:
@@ -170,7 +178,7 @@ std::string infeasible_reason(const VariantDesc& v, int path, const Problem& p) 
 
 int64_t variant_grid(const VariantDesc& v, int path, const Problem& p) {
   if (path == WTC_PATH_ROWS) return p.batch * cdiv(p.m, 128);
-  return p.batch * cdiv(p.m, v.tile_rows) * cdiv(p.n, 128);
+  return p.batch * cdiv(p.m, v.tile_rows) * cdiv(p.n, v.tile_n);
 }
 
 double estimate_us(const VariantDesc& v, int path, const Problem& p) {
@@ -179,7 +187,7 @@ double estimate_us(const VariantDesc& v, int path, const Problem& p) {
   const double elems = (double)p.batch * (double)p.m * (double)p.n;
   const double ab_bytes = (double)p.batch * ((double)p.m * p.k + (double)p.k * p.n) * isz;
   const double us_per_byte = 1e6 / (kHbmGBs * 1e9);
-  const double nT = (double)cdiv(p.n, 128);
+  const double nT = (double)cdiv(p.n, path == WTC_PATH_ROWS ? 128 : v.tile_n);
   if (path == WTC_PATH_ROWS) {
     const double blocks = (double)variant_grid(v, path, p);
     const double waves = std::ceil(blocks / cu);
@@ -189,13 +197,13 @@ double estimate_us(const VariantDesc& v, int path, const Problem& p) {
     const double t_hbm = (ab_bytes + elems * osz) * us_per_byte;
     return kLaunchUs + std::max(t_blocks, t_hbm);
   }
-  const TileCal& cal = kTileCal[v.id][in_class(p.in_dt)];
+  const TileCal& cal = kTileCal[cal_row(v.id)][in_class(p.in_dt)];
   const int epi = path == WTC_PATH_EXCHANGE ? 0 : (path == WTC_PATH_SPLIT ? 1 : 2);
   const double tiles = (double)variant_grid(v, path, p);
   const double waves = std::ceil(tiles / cu);
   const double f = clock_ghz(tiles / (waves * cu));
   const double nk = (double)cdiv(p.k * in_bytes(p.in_dt), 128);
-  const double kt_bytes = (double)(v.tile_rows + 128) * 128.0;  // A and B of one k-tile
+  const double kt_bytes = (double)(v.tile_rows + v.tile_n) * 128.0;  // A and B per 128 bytes of K
   auto wave_us = [&](double active) {
     const double kt = cal.kt_cyc + kt_bytes * active * f / kFeedGBs;
     return (cal.fixed_cyc[epi] + nk * kt) / (f * 1e3);

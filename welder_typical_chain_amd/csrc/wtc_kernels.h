@@ -1,5 +1,5 @@
 // wtc_kernels.h -- kernel parameter block and symbol table shared by the
-// HIP kernels (fused_matmul_softmax.hip, unfused_chain.hip) and the host
+// HIP kernels (fused_matmul_softmax.hip, wide_tile.hip, unfused_chain.hip) and the host
 // launcher (launch.hip).  Internal to the library; the public C-ABI is
 // include/wtc/wtc_hip.h.
 #pragma once
@@ -47,6 +47,13 @@ const void* zero_kernel_symbol();
 // Static LDS of the exchange-epilogue kernel of this wave layout.
 int chain_kernel_lds_bytes(int in_dt, int out_dt, int ks = 1);
 int chain_kernel_threads(int in_dt);  // workgroup size of chain_tile_kernel (every layout)
+
+// 256x256 tiles (wide_tile.hip): split epilogue (any output type) or f32
+// logits, 16-bit or fp8 inputs; NULL otherwise.  Same arguments as
+// chain_tile_kernel; the split path's statistics are [rows][nT] with nT the
+// 256-column tiles.
+const void* wide_kernel_symbol(int in_dt, int out_dt, int epi);
+int wide_kernel_threads();
 
 // One workgroup per 128-row block, two passes over N (K <= rows_kernel_max_k()).
 const void* rows_kernel_symbol(int in_dt, int out_dt);
