@@ -2,11 +2,13 @@
 wtc_matmul_softmax_tiles, against the CPU oracle (tolerances of
 tests/parity_util.py).
 
-Two shapes per input type: batch 2 x 300 x 1000 with a short K (ragged in
+Three shapes per input type: batch 2 x 300 x 1000 with a short K (ragged in
 every dimension: 300 rows are 2.3 tiles of 128 and 1.2 of 256, 1000 columns
-7.8 tiles of 128, K is 2 k-tiles with a ragged last one), and one batch of
-520 x 776 with K spanning 9 k-tiles (an odd count: both halves of the
-K loop's double-buffered step run, and the last runs alone).
+7.8 tiles of 128 and 3.9 of 256, K is 2 k-tiles with a ragged last one), the
+same with a negative logit scale (every kernel's row max becomes a min of
+its accumulators), and one batch of 520 x 776 with K spanning 9 k-tiles (an
+odd count: both halves of the K loop's double-buffered step run, and the
+last runs alone).
 """
 from __future__ import annotations
 
@@ -38,7 +40,7 @@ def _cases():
         for name, tiles, mask in _lib.variants(CODES[in_dt]):
             for path, pname in PATHS.items():
                 if mask & (1 << path):
-                    for shape in ("short", "long"):
+                    for shape in ("short", "long", "neg"):
                         out.append(pytest.param(in_dt, out_dt, name, tiles, pname, shape,
                                                 id=f"{in_dt}-{out_dt}-{name}-{pname}-{shape}"))
     return out
@@ -56,10 +58,11 @@ def _cases_or_empty():
 @pytest.mark.parametrize("in_dtype,out_dtype,variant,tiles,path,shape", _cases_or_empty())
 def test_variant_parity(native_lib, in_dtype, out_dtype, variant, tiles, path, shape):
     from welder_typical_chain_amd import _lib
-    if shape == "short":
+    if shape in ("short", "neg"):
         batch, m, n, k = 2, 300, 1000, SHORT_K[in_dtype]
     else:
         batch, m, n, k = 1, 520, 776, LONG_K[in_dtype]
+    scale = -0.8 if shape == "neg" else 0.8
     if path == "rows" and k > 128:
         with pytest.raises(_lib.WtcError) as ei:
             _lib.plan(batch, m, n, k, CODES[in_dtype], CODES[out_dtype], _lib.PATHS[path], tiles)
@@ -69,7 +72,7 @@ def test_variant_parity(native_lib, in_dtype, out_dtype, variant, tiles, path, s
     pl = _lib.plan(batch, m, n, k, CODES[in_dtype], CODES[out_dtype], _lib.PATHS[path], tiles, cu)
     assert pl["tiles"] == tiles and pl["path"] == _lib.PATHS[path]
     dist = "xorshift_uniform" if in_dtype == "f32" else "normal"
-    cfg = ChainConfig("variant", batch, m, n, k, in_dtype, out_dtype, dist, 0.3, logit_scale=0.8)
+    cfg = ChainConfig("variant", batch, m, n, k, in_dtype, out_dtype, dist, 0.3, logit_scale=scale)
     print(f"\n[gpu-case] {variant} {path} {in_dtype}->{out_dtype} {batch}x{m}x{n}x{k}", flush=True)
     inp = O.make_inputs(cfg, seed=21)
     out = run_chain(inp, in_dtype, out_dtype, path=path, batched=batch > 1, tiles=tiles)

@@ -28,6 +28,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "device_common.h"
 #include "tile_layout.h"
 #include "wtc_kernels.h"
@@ -373,46 +375,66 @@ chain_wide_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
     }
   };
   if constexpr (EPI == kEpiSplit) {
-    // y = c2 * acc (log2 domain); columns past N count as -inf
+    // y = c2 * acc (log2 domain); columns past N (ragged last tile only)
+    // count as -inf.  Instantiated for full tiles and for both signs of c2,
+    // so that pass 1 is a max (c2 >= 0) or a min (c2 < 0) of the raw
+    // accumulators and pass 2 one fma per exponential.
     const int nvalid = N32 - n0 < (uint32_t)kTN ? (int)(N32 - n0) : kTN;
-    auto y_of = [&](int mt, int j, int v) {
-      const int n_loc = wn * 128 + j * 32 + acc_i(lane, v);
-      return n_loc < nvalid ? acc[mt][j][v] * p.c2 : -INFINITY;
-    };
+    auto split_epi = [&](auto full_c, auto neg_c) {
+      constexpr bool FULL = decltype(full_c)::value;
+      constexpr bool NEG = decltype(neg_c)::value;
+      constexpr float kNone = NEG ? INFINITY : -INFINITY;
+      auto valid = [&](int j, int v) { return FULL || wn * 128 + j * 32 + acc_i(lane, v) < nvalid; };
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-      float mx = -INFINITY;
+      for (int mt = 0; mt < 4; ++mt) {
+        float ex = kNone;
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < 4; ++j)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) mx = fmaxf(mx, y_of(mt, j, v));
-      mx = wave_xor32_max(mx);
-      if (lane < 32) wred[wn * kTM + wm * 128 + mt * 32 + jr] = mx;
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    __syncthreads();
-    tmax[t] = fmaxf(wred[t], wred[kTM + t]);  // finite: every tile has a column inside N
-    __syncthreads();
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-      const int m_loc = wm * 128 + mt * 32 + jr;
-      const float tm = tmax[m_loc];
-      float sm = 0.0f;
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          f32x4 e;
-#pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            e[u] = __builtin_amdgcn_exp2f(y_of(mt, j, 4 * g + u) - tm);
-            sm += e[u];
+          for (int v = 0; v < 16; ++v) {
+            const float a = valid(j, v) ? acc[mt][j][v] : ex;
+            ex = NEG ? fminf(ex, a) : fmaxf(ex, a);
           }
-          if (L::ROUNDS == 1) stage_quad(m_loc, wn * 128 + j * 32 + acc_i(lane, 4 * g), e);
-        }
-      sm = wave_xor32_sum(sm);
-      if (lane < 32) wred[wn * kTM + m_loc] = sm;
-      __builtin_amdgcn_sched_barrier(0);
+        const float o = __shfl_xor(ex, 32);
+        ex = NEG ? fminf(ex, o) : fmaxf(ex, o);
+        // every column of this wave past N: -inf (exp2 of it is 0)
+        if (lane < 32) wred[wn * kTM + wm * 128 + mt * 32 + jr] = ex == kNone ? -INFINITY : ex * p.c2;
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      __syncthreads();
+      tmax[t] = fmaxf(wred[t], wred[kTM + t]);  // finite: every tile has a column inside N
+      __syncthreads();
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
+        const int m_loc = wm * 128 + mt * 32 + jr;
+        const float ntm = -tmax[m_loc];
+        float sm = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            f32x4 e;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+              const float x = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[mt][j][4 * g + u], p.c2, ntm));
+              e[u] = valid(j, 4 * g + u) ? x : 0.0f;
+              sm += e[u];
+            }
+            if (L::ROUNDS == 1) stage_quad(m_loc, wn * 128 + j * 32 + acc_i(lane, 4 * g), e);
+          }
+        sm = wave_xor32_sum(sm);
+        if (lane < 32) wred[wn * kTM + m_loc] = sm;
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    };
+    using T = std::true_type;
+    using F = std::false_type;
+    if (nvalid == kTN) {
+      if (p.c2 >= 0.0f) split_epi(T{}, F{});
+      else split_epi(T{}, T{});
+    } else {
+      if (p.c2 >= 0.0f) split_epi(F{}, F{});
+      else split_epi(F{}, T{});
     }
     __syncthreads();
     store_stat(p.partial + ((int64_t)rbg * kTM + t) * nT32 + nt, tmax[t], wred[t] + wred[kTM + t]);
@@ -445,7 +467,7 @@ chain_wide_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
               if constexpr (EPI == kEpiSplit) {
                 const int n_loc = wn * 128 + j * 32 + acc_i(lane, v);
                 const int nvalid = N32 - n0 < (uint32_t)kTN ? (int)(N32 - n0) : kTN;
-                x[u] = n_loc < nvalid ? __builtin_amdgcn_exp2f(acc[mt][j][v] * p.c2 - tm) : 0.0f;
+                x[u] = n_loc < nvalid ? __builtin_amdgcn_exp2f(__builtin_fmaf(acc[mt][j][v], p.c2, -tm)) : 0.0f;
               } else {
                 x[u] = acc[mt][j][v] * p.lin_scale;
               }
