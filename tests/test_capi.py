@@ -100,7 +100,7 @@ def test_plan_headline_and_configs(L):
 
 F16, BF16, FP8, F32 = _lib.DTYPE_F16, _lib.DTYPE_BF16, _lib.DTYPE_FP8_E4M3, _lib.DTYPE_F32
 T128 = {F16: [128, 128, 64, 2, 16], BF16: [128, 128, 64, 2, 16], FP8: [128, 128, 128, 2, 16]}
-KS2 = {F16: [128, 128, 64, 2, 32], BF16: [128, 128, 64, 2, 32], FP8: [128, 128, 128, 2, 32]}
+LDR = {F16: [128, 128, 64, 2, 32], BF16: [128, 128, 64, 2, 32], FP8: [128, 128, 128, 2, 32]}
 T256 = {F16: [256, 128, 64, 2, 32], BF16: [256, 128, 64, 2, 32], FP8: [256, 128, 128, 2, 32]}
 W256 = {F16: [256, 256, 32, 4, 64], BF16: [256, 256, 32, 4, 64], FP8: [256, 256, 64, 4, 64]}
 ROWS = [128, 128, 128, 2, 16]
@@ -114,9 +114,9 @@ def test_variant_table(L):
                       1 << _lib.PATH_ROWS)
     for dt in (F16, BF16):
         vs = _lib.variants(dt)
-        assert [v[1] for v in vs] == [T128[dt], KS2[dt], T256[dt], ROWS, W256[dt]]
+        assert [v[1] for v in vs] == [T128[dt], LDR[dt], T256[dt], ROWS, W256[dt]]
         assert [v[2] for v in vs] == [ex | sp | un, ex | sp | un, sp | un, ro, sp | un]
-    assert [v[1] for v in _lib.variants(FP8)] == [T128[FP8], KS2[FP8], T256[FP8], W256[FP8]]
+    assert [v[1] for v in _lib.variants(FP8)] == [T128[FP8], LDR[FP8], T256[FP8], W256[FP8]]
     assert [v[1] for v in _lib.variants(F32)] == [[128, 128, 32, 2, 32]]
     assert len({v[0] for dt in (F16, FP8, F32) for v in _lib.variants(dt)}) == 6
     assert L.wtc_list_variants(9, None, None, None, 0) == -1
@@ -126,19 +126,18 @@ def test_variant_table(L):
 # where the cost model picks the measured fastest (variant, path) on MI355X
 # (back-to-back calls); tests/test_cost_model.py scores every shape.
 MEASURED_BEST = [
-    ((1, 2048, 2048, 1024, F16, F16), KS2[F16], _lib.PATH_EXCHANGE),   # C2: 15.5 vs 15.8 us
-    ((1, 2048, 2048, 64, F16, F16), T128[F16], _lib.PATH_EXCHANGE),    # 8.1 vs 8.9
-    ((1, 2048, 2048, 256, F16, F16), T128[F16], _lib.PATH_EXCHANGE),   # 9.6 vs 9.7
-    ((1, 8192, 128, 64, F16, F16), T128[F16], _lib.PATH_EXCHANGE),     # 5.6 vs 6.1
-    ((1, 4096, 4096, 1024, F16, F16), W256[F16], _lib.PATH_SPLIT),     # 53.3 vs 64.3
-    ((1, 2048, 8192, 512, F16, F16), W256[F16], _lib.PATH_SPLIT),      # 41.2 vs 52.0
-    ((8, 2048, 2048, 128, F16, F16), ROWS, _lib.PATH_ROWS),            # 50.0 vs split 56.9
-    ((16, 512, 512, 64, F16, F16), T128[F16], _lib.PATH_EXCHANGE),     # 7.6 vs 8.2
-    ((1, 4096, 2048, 128, F16, F16), T256[F16], _lib.PATH_SPLIT),      # 22.2 vs 24.6
-    ((1, 640, 8192, 4096, F16, F16), T256[F16], _lib.PATH_SPLIT),      # 62.5 vs 69.8 (96 wide tiles: 84.7)
-    ((64, 2048, 2048, 128, F16, F16), ROWS, _lib.PATH_ROWS),           # C3: 253 vs 476
-    ((1, 1024, 32768, 4096, BF16, BF16), W256[BF16], _lib.PATH_SPLIT),  # C4: 257 vs 292
-    ((1, 8192, 8192, 4096, FP8, F16), W256[FP8], _lib.PATH_SPLIT),     # C5: 260 vs 347
+    ((1, 2048, 2048, 1024, F16, F16), LDR[F16], _lib.PATH_EXCHANGE),   # C2: 14.6 vs 16.4 us
+    ((1, 2048, 2048, 64, F16, F16), T128[F16], _lib.PATH_EXCHANGE),    # 8.1 vs 8.5
+    ((1, 2048, 2048, 256, F16, F16), T128[F16], _lib.PATH_EXCHANGE),   # 9.2 vs 9.4
+    ((1, 8192, 128, 64, F16, F16), T128[F16], _lib.PATH_EXCHANGE),     # 5.7 vs 5.8
+    ((1, 4096, 4096, 1024, F16, F16), W256[F16], _lib.PATH_SPLIT),     # 52.5 vs 64.2
+    ((1, 2048, 8192, 512, F16, F16), W256[F16], _lib.PATH_SPLIT),      # 40.1 vs 47.6
+    ((8, 2048, 2048, 128, F16, F16), ROWS, _lib.PATH_ROWS),            # 50.3 vs split 54.3
+    ((16, 512, 512, 64, F16, F16), T128[F16], _lib.PATH_EXCHANGE),     # 7.5 vs 8.0
+    ((1, 4096, 2048, 128, F16, F16), T256[F16], _lib.PATH_SPLIT),      # 22.2 vs 24.4
+    ((64, 2048, 2048, 128, F16, F16), ROWS, _lib.PATH_ROWS),           # C3: 250 vs 454
+    ((1, 1024, 32768, 4096, BF16, BF16), W256[BF16], _lib.PATH_SPLIT),  # C4: 257 vs 293
+    ((1, 8192, 8192, 4096, FP8, F16), W256[FP8], _lib.PATH_SPLIT),     # C5: 258 vs 347
 ]
 
 
@@ -237,7 +236,7 @@ def compile_chain(L, path: Path, out: Path, tiles, fused=1, errsize=4096):
 
 
 EXPECT = {  # config -> (tiles of the variant the solver ranks first, its path)
-    "C1": ([128, 128, 32, 2, 32], "exchange"), "C2": (KS2[F16], "exchange"), "C3": (ROWS, "rows"),
+    "C1": ([128, 128, 32, 2, 32], "exchange"), "C2": (LDR[F16], "exchange"), "C3": (ROWS, "rows"),
     "C4": (W256[BF16], "split"), "C5": (W256[FP8], "split"),
 }
 

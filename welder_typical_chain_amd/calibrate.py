@@ -182,7 +182,7 @@ def time_case(shape, tiles, path, device, target_ms=20.0):
 # values.
 
 _VARIANT_IDS = {"tile128x128_wave64x32": 0, "tile128x128_wave64x64": 0,
-                "tile128x128_wave64x64_ksplit2": 1, "tile256x128_wave64x64": 2,
+                "tile128x128_wave64x64_loaders": 1, "tile256x128_wave64x64": 2,
                 "rows128_wave64x32_k128": 3, "tile256x256_wave128x128": 4}
 # tile rows and columns per tile variant id
 _TILE = {0: (128, 128), 1: (128, 128), 2: (256, 128), 4: (256, 256)}

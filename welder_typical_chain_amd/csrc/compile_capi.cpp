@@ -31,7 +31,7 @@ int rescale_waves_per_row(int64_t rows_total, int cu_count);
 // Compute units of the current device, or `fallback` when no GPU is visible.
 int device_cu_count(int fallback);
 // Dynamic LDS bytes the launcher adds to the exchange kernel of wave layout ks.
-int exchange_lds_pad(int in_dt, int out_dt, int ks);
+int exchange_lds_pad(int in_dt, int out_dt, int loaders);
 
 static std::string library_path() {
   Dl_info info{};
@@ -183,9 +183,9 @@ static int compile_impl(const char* input_mlir_path, const char* out_dir, int64_
     int block = 256;
   };
   // chain_tile_kernel<in, out, epi, PF = 3, tile rows, ks>
-  auto chain_sym = [](int in, int out, int epi, int tm = 128, int ks = 1) {
+  auto chain_sym = [](int in, int out, int epi, int tm = 128, int lw = 0) {
     return "_ZN3wtc17chain_tile_kernelILi" + std::to_string(in) + "ELi" + std::to_string(out) +
-           "ELi" + std::to_string(epi) + "ELi3ELi" + std::to_string(tm) + "ELi" + std::to_string(ks) + "E";
+           "ELi" + std::to_string(epi) + "ELi3ELi" + std::to_string(tm) + "ELi" + std::to_string(lw) + "E";
   };
   // chain_wide_kernel<in, out, epi>: the 256x256 tiles
   auto wide_sym = [](int in, int out, int epi) {
@@ -197,9 +197,9 @@ static int compile_impl(const char* input_mlir_path, const char* out_dir, int64_
   auto tile_kern = [&](int out, const std::string& out_name, int epi, const std::string& epi_name) {
     if (wide) return std::make_pair("chain_wide_kernel<" + kin + "," + out_name + "," + epi_name + ",256x256>",
                                     wide_sym(in_code, out, epi));
-    const std::string layout = std::to_string(var.tile_rows) + "x128" + (var.ks == 2 ? ",ksplit2" : "");
+    const std::string layout = std::to_string(var.tile_rows) + "x128" + (var.loaders ? ",loaders" : "");
     return std::make_pair("chain_tile_kernel<" + kin + "," + out_name + "," + epi_name + "," + layout + ">",
-                          chain_sym(in_code, out, epi, var.tile_rows, var.ks));
+                          chain_sym(in_code, out, epi, var.tile_rows, var.loaders));
   };
   const std::string out_t = "ILi" + std::to_string(out_code) + "E";
   std::vector<K> ks;
@@ -212,9 +212,9 @@ static int compile_impl(const char* input_mlir_path, const char* out_dir, int64_
                   grid, 0, rows_kernel_threads()});
   } else if (path == WTC_PATH_EXCHANGE) {
     ks.push_back({"chain_tile_kernel<" + kin + "," + kout + ",exchange,128x128" +
-                      (var.ks == 2 ? ",ksplit2" : "") + ">",
-                  chain_sym(in_code, out_code, 0, 128, var.ks), grid,
-                  exchange_lds_pad(in_code, out_code, var.ks), tile_threads});
+                      (var.loaders ? ",loaders" : "") + ">",
+                  chain_sym(in_code, out_code, 0, 128, var.loaders), grid,
+                  exchange_lds_pad(in_code, out_code, var.loaders), tile_threads});
   } else if (path == WTC_PATH_SPLIT) {
     const auto tk = tile_kern(out_code, kout, 1, "split");
     ks.push_back({tk.first, tk.second, grid, 0, tile_threads});

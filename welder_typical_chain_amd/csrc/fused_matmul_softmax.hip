@@ -7,11 +7,10 @@
 // chain spec mlir/matmul_softmax_chain_f16_native.mlir:7-95).
 //
 // One workgroup owns a TM x 128 output tile (TM = 128; 256 on the split
-// path of large problems).  16-bit and fp8 inputs: 512 threads = 8 waves of
-// 64 rows each (64x32 blocks in a 2x4 grid for TM = 128, 64x64 in a 4x2 grid
-// for TM = 256), 2 waves per SIMD; k-tiles of 128 bytes of K stream through
-// an LDS ring filled by direct-to-LDS buffer loads, B stays K-major in LDS
-// and its MFMA operands are read with LDS transpose reads.  f32 inputs:
+// path of large problems).  16-bit and fp8 inputs: 512 threads = 8 waves, 2
+// per SIMD (the wave layouts are described at Cfg); k-tiles of 128 bytes of
+// K stream through an LDS ring filled by direct-to-LDS buffer loads, B stays
+// K-major in LDS and its MFMA operands are read with LDS transpose reads.  f32 inputs:
 // 256 threads = 4 waves in a 2x2 grid; k-tiles are loaded `PF` ahead into
 // registers (out-of-range lanes read zero, so the outstanding-load count
 // stays exact), B is transposed in registers, and a two-stage LDS ring feeds
@@ -52,42 +51,40 @@ constexpr int BN = 128;
 constexpr int A_STAGE_BYTES = BM * kKTileBytes;                  // 16 KiB
 constexpr int STAGE_BYTES = A_STAGE_BYTES + BN * kKTileBytes;    // 32 KiB
 
-// Per input type and tile height TM: 16-bit and fp8 inputs stream through a
-// ring of direct-to-LDS loads and run 8 waves (2 per SIMD: while one waits to
-// issue a load, the other issues MFMAs), each owning 64 rows -- a 64x32 block
-// of a 128-row tile (4 stages of 32 KiB) or a 64x64 block of a 256-row tile
-// (3 stages of 48 KiB, for the split path of large problems: a quarter less
-// L2 and a third less LDS traffic per MFMA).  f32 goes through a 2-stage ring
-// filled from registers with 4 waves of 64x64 (TM = 128 only).  Every ring
-// keeps k-tiles kt+1 .. kt+3 in flight or landed while k-tile kt's fragments
-// are in registers, so 3 stages suffice when a stage may be refilled as soon
-// as its fragments have been read.
-//
-// KS = 2 (k-split, 128-row tiles of 16-bit and fp8 inputs): the 8 waves form
-// 2 x 2 x 2 (M x N x K); the two waves of a (M, N) pair each own the same
-// 64x64 block and run half of every k-tile's MFMA k-steps, so each wave reads
-// 64 A rows and 64 B columns per k-step instead of 64 and 32 -- a third less
-// LDS read traffic per MFMA than 64x32 blocks.  After the K loop each wave
-// hands the partner its partial sums of one 32-column half and adds the
-// partner's of the other (one LDS round trip), leaving every wave a 64x32
-// block, which is the epilogue's layout for KS = 1 as well.
-template <int IN_DT, int TM = 128, int KS = 1> struct Cfg {
+// Per input type, tile height TM and wave layout LW.  16-bit and fp8 inputs
+// stream through a ring of direct-to-LDS loads with 8 waves, 2 per SIMD:
+//   LW = 0, TM = 128: a 2x4 grid of 64x32 blocks; every wave issues its
+//     share of each k-tile's loads between its MFMAs (while one wave of a
+//     SIMD waits to issue a load, the other issues MFMAs); 4 stages of 32 KiB.
+//   LW = 0, TM = 256: a 4x2 grid of 64x64 blocks, 3 stages of 48 KiB (the
+//     split path of large problems: a quarter less L2 and a third less LDS
+//     traffic per MFMA).
+//   LW = 1, TM = 128 (loader waves): 4 MFMA waves, one per SIMD, in a 2x2
+//     grid of 64x64 blocks (a third less LDS read traffic per MFMA than
+//     64x32 blocks), and 4 loader waves that issue every direct-to-LDS load,
+//     so an MFMA wave never waits for the memory pipeline to take a load.
+//     All 8 waves share the epilogue's polling, merging and stores.
+// f32 goes through a 2-stage ring filled from registers with 4 waves of
+// 64x64 (TM = 128, LW = 0 only).  Every ring keeps k-tiles kt+1 .. kt+3 in
+// flight or landed while k-tile kt's fragments are in registers, so 3 stages
+// suffice when a stage may be refilled as soon as its fragments have been read.
+template <int IN_DT, int TM = 128, int LW = 0> struct Cfg {
   static constexpr bool kDma = IN_DT == DT_F16 || IN_DT == DT_BF16 || IN_DT == DT_FP8;
   static_assert(TM == 128 || (TM == 256 && kDma), "tile height");
-  static_assert(KS == 1 || (KS == 2 && kDma && TM == 128), "k-split layout");
+  static_assert(LW == 0 || (LW == 1 && kDma && TM == 128), "loader-wave layout");
+  static constexpr bool kLoaders = LW == 1;
   static constexpr int kBM = TM;
-  static constexpr int kKS = KS;
-  static constexpr int kWavesM = kDma ? TM / 64 : 2;     // waves along M
-  static constexpr int kWavesN = kDma ? 8 / kWavesM / KS : 2;  // waves along N (K loop)
-  static constexpr int kWaves = kWavesM * kWavesN * KS;
+  static constexpr int kWavesM = kDma ? TM / 64 : 2;                         // MFMA waves along M
+  static constexpr int kWavesN = kLoaders ? 2 : (kDma ? 8 / kWavesM : 2);   // ... along N
+  static constexpr int kMfmaWaves = kWavesM * kWavesN;
+  static constexpr int kWaves = kLoaders ? 2 * kMfmaWaves : kMfmaWaves;
+  static constexpr int kLoadWaves = kLoaders ? kWaves - kMfmaWaves : kWaves;  // issue the loads
   static constexpr int kThreads = 64 * kWaves;
-  static constexpr int kNT = BN / kWavesN / 32;          // 32-column subtiles per wave (K loop)
-  static constexpr int kNTE = kNT / KS;                  // ... in the epilogue
-  static constexpr int kWavesNE = kWavesN * KS;          // waves along N in the epilogue
-  // MFMA k-steps of one k-tile per wave (16-bit: 4 of 16; fp8: 2 of 64)
-  static constexpr int kKSteps = (IN_DT == DT_FP8 ? 2 : 4) / KS;
-  static constexpr int kABlocksPerWave = TM / 8 / kWaves;  // 1 KiB load blocks of A
-  static constexpr int kBBlocksPerWave = 16 / kWaves;      // ... and of B
+  static constexpr int kNT = BN / kWavesN / 32;  // 32-column subtiles per MFMA wave
+  // MFMA k-steps of one k-tile (16-bit: 4 of 16; fp8: 2 of 64)
+  static constexpr int kKSteps = IN_DT == DT_FP8 ? 2 : 4;
+  static constexpr int kABlocksPerWave = TM / 8 / kLoadWaves;  // 1 KiB load blocks of A
+  static constexpr int kBBlocksPerWave = 16 / kLoadWaves;      // ... and of B
   static constexpr int kAStageBytes = TM * kKTileBytes;
   static constexpr int kStageBytes = kAStageBytes + BN * kKTileBytes;
   static constexpr int kStages = kDma ? (TM == 256 ? 3 : 4) : 2;
@@ -104,21 +101,17 @@ constexpr int kStagePitch = BN + 4;
 // different banks), for up to 64 column tiles.
 constexpr int kLsePitch = 129;
 
-template <int IN_DT, int OUT_DT, int TM = 128, int KS = 1, bool XCH = false> struct EpiLayout {
+template <int IN_DT, int OUT_DT, int TM = 128, int LW = 0, bool XCH = false> struct EpiLayout {
   static constexpr int STAGING = TM * kStagePitch * 4;
   // exchange path: the log-sum-exp table follows the staged tile
   static constexpr int LSE_OFF = (STAGING + 255) / 256 * 256;
   static constexpr int LSE_END = XCH ? LSE_OFF + 64 * kLsePitch * 4 : STAGING;
-  static constexpr int RING = Cfg<IN_DT, TM, KS>::kRingBytes;
-  // k-split: each wave's half-block of partial sums (64 x 32 f32) passes
-  // through LDS once, in the ring after the last k-tile
-  static constexpr int KMERGE = KS == 2 ? 8 * 64 * 32 * 4 : 0;
-  static_assert(KMERGE <= RING, "k-split merge area");
+  static constexpr int RING = Cfg<IN_DT, TM, LW>::kRingBytes;
   static constexpr int UNION = LSE_END > RING ? LSE_END : RING;
   static constexpr int RED_OFF = (UNION + 255) / 256 * 256;
-  // wstat[kWavesNE][TM] (float2), factor[kWavesNE][TM] (float), then the
+  // wstat[kWavesN][TM] (float2), factor[kWavesN][TM] (float), then the
   // exchange path's tile log-sum-exps [TM] (float) and slot generations [64]
-  static constexpr int TOTAL = RED_OFF + 3 * Cfg<IN_DT, TM, KS>::kWavesNE * TM * 4 + TM * 4 + 64 * 4;
+  static constexpr int TOTAL = RED_OFF + 3 * Cfg<IN_DT, TM, LW>::kWavesN * TM * 4 + TM * 4 + 64 * 4;
   static_assert(TOTAL <= 160 * 1024, "LDS");
 };
 
@@ -410,27 +403,25 @@ struct KTileFrags {
 // 32 rows (4096 bytes: the A swizzle depends on row/2 mod 8 only), the
 // k-step and half (quad) of B add whole k-rows (its swizzle depends on k mod
 // 4, fp8: k/2 mod 4 only) -- so a step's reads need these few address
-// registers instead of one per read.  The wave runs k-steps s0 .. s0+KSW-1 of
-// each k-tile (s0 = 0 without a k-split).  A: per k-step s the chunk 2s +
-// lane/32 (16-bit) or, for fp8, entry 2s + hh for chunk 4s + 2(lane/32) + hh.
-// B: per n-subtile nt (first column nw + ((nt + rot) % NTN) * 32: a k-split
-// wave starts with its own epilogue slice), k-step s0, half / quad 0.
+// registers instead of one per read.  A: per k-step s the chunk 2s + lane/32
+// (16-bit) or, for fp8, entry 2s + hh for chunk 4s + 2(lane/32) + hh.  B: per
+// n-subtile nt (first column nw + nt * 32), k-step 0, half / quad 0.
 template <bool F8, int NTN, int KSW, int ASTAGE>
 struct FragBase {
   static constexpr int NA = F8 ? 2 * KSW : KSW;
   uint32_t a[NA], b[NTN];
-  __device__ inline void init(int lane, int wm, int nw, int rot, int s0) {
+  __device__ inline void init(int lane, int wm, int nw) {
     const int r = frag_row(lane);
 #pragma unroll
     for (int i = 0; i < NA; ++i) {
-      const int c = F8 ? 4 * (s0 + (i >> 1)) + 2 * (lane >> 5) + (i & 1) : frag_chunk(lane, s0 + i);
+      const int c = F8 ? 4 * (i >> 1) + 2 * (lane >> 5) + (i & 1) : frag_chunk(lane, i);
       a[i] = (uint32_t)a_lds_offset(wm * 64 + r, c);
     }
 #pragma unroll
     for (int nt = 0; nt < NTN; ++nt) {
-      const int nb = nw + ((nt + rot) % NTN) * 32;
-      b[nt] = (uint32_t)(ASTAGE + (F8 ? btr8_offset(btr8_k(s0, 0, lane), btr8_n(nb, lane))
-                                      : btr_offset(btr_k(s0, 0, lane), btr_n(nb, lane))));
+      const int nb = nw + nt * 32;
+      b[nt] = (uint32_t)(ASTAGE + (F8 ? btr8_offset(btr8_k(0, 0, lane), btr8_n(nb, lane))
+                                      : btr_offset(btr_k(0, 0, lane), btr_n(nb, lane))));
     }
   }
 };
@@ -586,20 +577,19 @@ constexpr int step_groups(int loads, int reads, int mfmas) {
 // workgroup count (gridDim.x would be read from the hidden kernel arguments
 // in memory).  Sizes and per-batch strides are 32-bit: the launcher keeps one
 // batch slice of A, B and out below 2 GiB.
-template <int IN_DT, int OUT_DT, int EPI, int PF, int TM, int KS>
-__global__ void __launch_bounds__((Cfg<IN_DT, TM, KS>::kThreads), 1)
+template <int IN_DT, int OUT_DT, int EPI, int PF, int TM, int LW>
+__global__ void __launch_bounds__((Cfg<IN_DT, TM, LW>::kThreads), 1)
 chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32_t N32,
                   uint32_t K32, uint32_t lda32, uint32_t ldb32, uint32_t nT32, uint32_t nRB32,
                   uint32_t a_bs32, uint32_t b_bs32, uint32_t grid32, const ChainParams p) {
-  using C = Cfg<IN_DT, TM, KS>;
-  using L = EpiLayout<IN_DT, OUT_DT, TM, KS, EPI == kEpiExchange>;
+  using C = Cfg<IN_DT, TM, LW>;
+  using L = EpiLayout<IN_DT, OUT_DT, TM, LW, EPI == kEpiExchange>;
   static_assert(EPI != kEpiExchange || TM == 128, "the exchange path runs 128-row tiles");
   constexpr int BM = TM;  // tile rows
   constexpr int NT = C::kThreads;
-  constexpr int WNK = C::kWavesN;  // waves along N in the K loop
-  constexpr int NTN = C::kNT;      // 32-column subtiles per wave in the K loop
-  constexpr int WN = C::kWavesNE;  // ... and in the epilogue
-  constexpr int NTE = C::kNTE;
+  constexpr int WN = C::kWavesN;  // MFMA waves along N
+  constexpr int NTN = C::kNT;     // 32-column subtiles per MFMA wave
+  constexpr bool LDW = C::kLoaders;
   __shared__ __attribute__((aligned(16))) uint8_t smem[L::TOTAL];
   float2* wstat = reinterpret_cast<float2*>(smem + L::RED_OFF);  // [WN][BM] wave (max, sum)
   float* factor = reinterpret_cast<float*>(wstat + WN * BM);     // [WN][BM]
@@ -607,11 +597,12 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int wave = t >> 6;
-  // wave = (wm * WNK + wn_k) * KS + wk: k-split partners are adjacent waves
-  const int wk = wave % KS;
-  const int wm = wave / KS / WNK, wn_k = wave / KS % WNK;
-  const int wn = wn_k * KS + wk;  // the wave's column slice in the epilogue
-  const int nw = wn * 32 * NTE;   // first column of that slice
+  // MFMA wave = wm * WN + wn owns rows wm*64 .. +63 and columns nw .. nw +
+  // 32*NTN - 1 of the tile; with loader waves (LW = 1) waves kMfmaWaves ..
+  // issue the loads and own no block (their wm, wn are not used).
+  const int wm = wave / WN, wn = wave % WN;
+  const int nw = wn * 32 * NTN;  // first column of the wave's block
+  const bool loader = LDW && __builtin_amdgcn_readfirstlane(wave) >= C::kMfmaWaves;
 
   uint32_t rbg, nt;  // row block across batches, column tile
   tile_of_block(blockIdx.x, grid32, grid32 / nT32, nT32, &rbg, &nt);
@@ -653,9 +644,9 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
     // (kt+3) % S -- free by then for S = 3 and S = 4 -- with k-tile kt+3,
     // read k-tile kt+1's fragments into registers and run k-tile kt's MFMAs
     // from the fragments read one iteration earlier: the MFMAs never wait
-    // for LDS, and k-tiles kt+2, kt+3 stay in flight.  Each wave issues LPT
-    // loads per k-tile.  Loads past the last k-tile read zeros into stages
-    // that are never used.
+    // for LDS, and k-tiles kt+2, kt+3 stay in flight.  Each loading wave (all
+    // waves, or the loader waves of LW = 1) issues LPT loads per k-tile.
+    // Loads past the last k-tile read zeros into stages that are never used.
     constexpr int S = C::kStages;
     constexpr int D = 3;  // k-tiles requested ahead of the one whose MFMAs run
     static_assert(S >= D, "ring depth");
@@ -664,17 +655,17 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
     constexpr bool F8 = IN_DT == DT_FP8;
     using Plan = DmaPlan<IN_DT, C::kABlocksPerWave, C::kBBlocksPerWave, ASTAGE>;
     constexpr int LPT = Plan::LPT;                            // loads per wave per k-tile
-    constexpr int KSW = C::kKSteps;  // MFMA k-steps of a k-tile this wave runs
+    constexpr int KSW = C::kKSteps;  // MFMA k-steps of a k-tile
     constexpr int RPT = F8 ? KSW * (4 + 4 * NTN) : KSW * (2 + 2 * NTN);  // fragment reads
     constexpr int MPT = KSW * 2 * NTN;                                  // MFMAs
-    // G groups per k-tile step: the fewest (>= LPT) that divide the reads
-    // and the MFMAs evenly
+    // G groups per k-tile step: the fewest (>= LPT) that divide the reads and
+    // the MFMAs evenly (with loader waves the MFMA waves' groups hold no load,
+    // and the same interleave of reads and MFMAs keeps the matrix core fed)
     constexpr int G = step_groups(LPT, RPT, MPT);
     static_assert(G > 0, "k-tile step groups");
     using Frags = std::conditional_t<F8, KTileFrags8<NTN, KSW>, KTileFrags<NTN, KSW>>;
     FragBase<F8, NTN, KSW, ASTAGE> fb;
-    // K-loop subtiles: the wave's epilogue slice first, then (k-split) the partner's
-    fb.init(lane, wm, wn_k * 32 * NTN, wk * NTE, wk * KSW);
+    fb.init(lane, wm, nw);
     auto read_piece = [&](const uint8_t* st, int i, Frags& f) {
       if constexpr (F8)
         read_frag_piece8<NTN, KSW, ASTAGE>(st, fb, i, f);
@@ -687,27 +678,42 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
       else
         mma_piece<IN_DT, NTN, KSW>(f, i, acc);
     };
-    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+    // the wave's index among the loading waves
+    const int wave_u = __builtin_amdgcn_readfirstlane(wave) - (loader ? C::kMfmaWaves : 0);
     Plan d;
     d.init(a_in + (uint64_t)bt * a_bs32, b_in + (uint64_t)bt * b_bs32, a_bs32, b_bs32,
            (uint32_t)row0, (uint32_t)n0, M32, N32, K32, lda32, ldb32, wave_u, lane);
     const uint32_t lds0 = (uint32_t)(uintptr_t)(WTC_LDS uint8_t*)smem;
     if (nk == 0) load_gen0();
     if (nk > 0) {
+      if (!LDW || loader) {
 #pragma unroll
-      for (int q = 0; q < D; ++q) d.issue(lds0 + q * STAGE, q);
+        for (int q = 0; q < D; ++q) d.issue(lds0 + q * STAGE, q);
+      }
       load_gen0();  // newer than the k-tile loads: only makes the waits below stricter
       wait_loads_barrier<LPT * (D - 1)>();  // k-tile 0 landed
+      if (loader) {
+        // Loader waves: the same waits and barriers as the MFMA waves, one
+        // per k-tile; after each, k-tile kt+3 into the stage kt+3 % S.
+        for (int kt = 0; kt < nk; ++kt) {
+          wait_loads_barrier<LPT * (D - 2)>();
+          const uint32_t fill = lds0 + ((kt + D) % S) * STAGE;
+#pragma unroll
+          for (int j = 0; j < LPT; ++j) d.issue_one(fill, kt + D, j);
+        }
+        wait_loads_barrier<0>();
+      } else {
       Frags f0, f1;
 #pragma unroll
       for (int i = 0; i < RPT; ++i) read_piece(smem, i, f0);
-      // One k-tile step, in G groups of (a load of k-tile kt+3 in the first
-      // LPT groups, RPT/G fragment reads of k-tile kt+1, MPT/G MFMAs of
-      // k-tile kt).  A wave that issues a direct-to-LDS load stalls until the
-      // memory pipeline accepts it; spreading the MFMAs between the loads
-      // keeps the matrix core busy through those stalls.  sched_barrier pins
-      // the groups (MFMAs touch no memory, so the compiler would otherwise
-      // move them freely, also across s_barrier).
+      // One k-tile step, in G groups of (LW = 0: a load of k-tile kt+3 in
+      // the first LPT groups; RPT/G fragment reads of k-tile kt+1, MPT/G
+      // MFMAs of k-tile kt).  A wave that issues a direct-to-LDS load stalls
+      // until the memory pipeline accepts it; spreading the MFMAs between the
+      // loads keeps the matrix core busy through those stalls (with loader
+      // waves the MFMA waves never wait there).  sched_barrier pins the
+      // groups (MFMAs touch no memory, so the compiler would otherwise move
+      // them freely, also across s_barrier).
       auto step = [&](int kt, const Frags& cur, Frags& next) {
         __builtin_amdgcn_sched_barrier(0);
         wait_loads_barrier<LPT * (D - 2)>();  // k-tile kt+1 landed; kt's fragments read
@@ -716,7 +722,7 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
         const uint8_t* rd = smem + ((kt + 1) % S) * STAGE;
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-          if (g < LPT) d.issue_one(fill, kt + D, g);
+          if (!LDW && g < LPT) d.issue_one(fill, kt + D, g);
 #pragma unroll
           for (int i = 0; i < RPT / G; ++i) read_piece(rd, (RPT / G) * g + i, next);
 #pragma unroll
@@ -729,6 +735,7 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
         if (kt + 1 < nk) step(kt + 1, f1, f0);
       }
       wait_loads_barrier<0>();
+      }
     }
   } else if (nk == 0) {
     load_gen0();
@@ -779,45 +786,21 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
     }
   }
 
-  // ---- k-split: merge the partners' partial sums --------------------------
-  // Every wave has passed its last LDS read (the K loop ends with a wait and a
-  // barrier), so the ring is free.  Each wave stores its partial sums of the
-  // partner's slice (subtiles NTE .. NTN-1), lane-major, 16 bytes per lane
-  // per store, and adds the partner's partial sums of its own slice.
-  if constexpr (KS == 2) {
-    static_assert(NTN == 2 && NTE == 1, "k-split pairs share a 64x64 block");
-    f32x4* xch = reinterpret_cast<f32x4*>(smem);  // [wave][mt][4 quads][64 lanes]
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int g = 0; g < 4; ++g)
-        xch[(wave * 8 + mt * 4 + g) * 64 + lane] =
-            f32x4{acc[mt][1][4 * g], acc[mt][1][4 * g + 1], acc[mt][1][4 * g + 2], acc[mt][1][4 * g + 3]};
-    __syncthreads();
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const f32x4 v = xch[((wave ^ 1) * 8 + mt * 4 + g) * 64 + lane];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) acc[mt][0][4 * g + e] += v[e];
-      }
-  }
-
   // ---- epilogue --------------------------------------------------------------
   // Lane owns output rows m_loc(mt) = wm*64 + mt*32 + lane%32 and, for each
   // n-subtile j, the 16 columns n_loc = nw + j*32 + acc_i(lane, v).  Each
   // wave normalises its exponentials against the max of its own columns
   // (wave max m_w, sum s_w per row, kept in LDS); the tile's statistics and
   // the final scale factors are combined from those, so one LDS exchange
-  // serves both.
+  // serves both.  Loader waves (LW = 1) hold no block: they skip the
+  // per-wave statistics and the staging and take part in the rest.
   const int jr = acc_j(lane);
   const int nvalid = p.N - n0 < BN ? (int)(p.N - n0) : BN;  // columns of this tile inside N
   if constexpr (EPI == kEpiLogits) {
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-      for (int j = 0; j < NTE; ++j)
+      for (int j = 0; j < NTN; ++j)
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[mt][j][v] *= p.lin_scale;
   } else {
@@ -826,14 +809,14 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-        for (int j = 0; j < NTE; ++j)
+        for (int j = 0; j < NTN; ++j)
 #pragma unroll
           for (int v = 0; v < 16; ++v) acc[mt][j][v] *= p.c2;
     } else {
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-        for (int j = 0; j < NTE; ++j)
+        for (int j = 0; j < NTN; ++j)
 #pragma unroll
           for (int v = 0; v < 16; ++v) {
             const int n_loc = nw + j * 32 + acc_i(lane, v);
@@ -841,17 +824,17 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
           }
     }
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
+    for (int mt = 0; mt < (loader ? 0 : 2); ++mt) {
       float mx = -INFINITY;
 #pragma unroll
-      for (int j = 0; j < NTE; ++j)
+      for (int j = 0; j < NTN; ++j)
 #pragma unroll
         for (int v = 0; v < 16; ++v) mx = fmaxf(mx, acc[mt][j][v]);
       mx = wave_xor32_max(mx);
       const float base = mx == -INFINITY ? 0.0f : mx;  // every column of this wave past N
       float sm = 0.0f;
 #pragma unroll
-      for (int j = 0; j < NTE; ++j)
+      for (int j = 0; j < NTN; ++j)
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           const float e = __builtin_amdgcn_exp2f(acc[mt][j][v] - base);
@@ -914,9 +897,9 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
   // and, on the exchange path, precedes the wait for the other tiles.
   float* stg = reinterpret_cast<float*>(smem);
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt)
+  for (int mt = 0; mt < (loader ? 0 : 2); ++mt)
 #pragma unroll
-    for (int j = 0; j < NTE; ++j)
+    for (int j = 0; j < NTN; ++j)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int m_loc = wm * 64 + mt * 32 + jr;
@@ -927,8 +910,8 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
       }
 
   if constexpr (EPI != kEpiLogits) {
-    constexpr int P = NT / BM;  // threads per row (== WN)
-    static_assert(P == WN, "one thread per (row, wave column slice)");
+    constexpr int P = NT / BM;  // threads per row (WN, or 2 WN with loader waves)
+    static_assert(P % WN == 0 && (P & (P - 1)) == 0 && P <= 4, "threads per row");
     const int r = t / P, h = t % P;
     if constexpr (EPI == kEpiExchange) {
       __syncthreads();  // tlse and sgen are in place
@@ -1021,15 +1004,19 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
              (om == -INFINITY ? 0.0f : os * __builtin_amdgcn_exp2f(om - M));
         gm = M;
       }
-      // thread (r, h) owns the factor of row r, column slice of wave h:
+      // thread (r, h < WN) owns the factor of row r, column slice of wave h:
       // exp2(m_w - L) with L = max + log2(sum) the row's log-sum-exp
       const float row_lse = gm + __builtin_amdgcn_logf(gs);
-      const float mw = wstat[h * BM + r].x;
-      factor[h * BM + r] = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - row_lse);
+      if (h < WN) {
+        const float mw = wstat[h * BM + r].x;
+        factor[h * BM + r] = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - row_lse);
+      }
     } else {
       // split: exponentials relative to the tile max, as the statistics say
-      const float mw = wstat[h * BM + r].x;
-      factor[h * BM + r] = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - tile_stat(r).x);
+      if (h < WN) {
+        const float mw = wstat[h * BM + r].x;
+        factor[h * BM + r] = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - tile_stat(r).x);
+      }
     }
   }
   __syncthreads();
@@ -1060,7 +1047,7 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
     const int64_t m = row0 + row;
     const int64_t n = n0 + ch * EPC;
     if (m < p.M && n < p.N) {
-      const float f = EPI == kEpiLogits ? 1.0f : factor[(ch * EPC / (32 * NTE)) * BM + row];
+      const float f = EPI == kEpiLogits ? 1.0f : factor[(ch * EPC / (32 * NTN)) * BM + row];
       const float* src = stg + row * kStagePitch + ch * EPC;
       const f32x4 x0 = *reinterpret_cast<const f32x4*>(src) * f;
       if constexpr (OSZ == 4) {
@@ -1177,17 +1164,17 @@ __global__ void zero_words_kernel(uint32_t* __restrict__ p, int64_t n) {
 // -------------------------------------------------------------------------
 constexpr int kPF = 3;
 
-template <int IN_DT, int OUT_DT, int EPI, int TM, int KS>
+template <int IN_DT, int OUT_DT, int EPI, int TM, int LW>
 static const void* tile_kernel_ptr() {
-  return reinterpret_cast<const void*>(&chain_tile_kernel<IN_DT, OUT_DT, EPI, kPF, TM, KS>);
+  return reinterpret_cast<const void*>(&chain_tile_kernel<IN_DT, OUT_DT, EPI, kPF, TM, LW>);
 }
 
-template <int IN_DT, int EPI, int TM, int KS>
+template <int IN_DT, int EPI, int TM, int LW>
 static const void* by_out(int out_dt) {
   switch (out_dt) {
-    case DT_F32: return tile_kernel_ptr<IN_DT, DT_F32, EPI, TM, KS>();
-    case DT_F16: return tile_kernel_ptr<IN_DT, DT_F16, EPI, TM, KS>();
-    case DT_BF16: return tile_kernel_ptr<IN_DT, DT_BF16, EPI, TM, KS>();
+    case DT_F32: return tile_kernel_ptr<IN_DT, DT_F32, EPI, TM, LW>();
+    case DT_F16: return tile_kernel_ptr<IN_DT, DT_F16, EPI, TM, LW>();
+    case DT_BF16: return tile_kernel_ptr<IN_DT, DT_BF16, EPI, TM, LW>();
   }
   return nullptr;
 }
@@ -1195,7 +1182,18 @@ static const void* by_out(int out_dt) {
 template <int EPI>
 static const void* by_in(int in_dt, int out_dt) {
   switch (in_dt) {
-    case DT_F32: return by_out<DT_F32, EPI, 128, 1>(out_dt);
+    case DT_F32: return by_out<DT_F32, EPI, 128, 0>(out_dt);
+    case DT_F16: return by_out<DT_F16, EPI, 128, 0>(out_dt);
+    case DT_BF16: return by_out<DT_BF16, EPI, 128, 0>(out_dt);
+    case DT_FP8: return by_out<DT_FP8, EPI, 128, 0>(out_dt);
+  }
+  return nullptr;
+}
+
+// 128-row tiles with loader waves (16-bit and fp8 inputs).
+template <int EPI>
+static const void* loaders_by_in(int in_dt, int out_dt) {
+  switch (in_dt) {
     case DT_F16: return by_out<DT_F16, EPI, 128, 1>(out_dt);
     case DT_BF16: return by_out<DT_BF16, EPI, 128, 1>(out_dt);
     case DT_FP8: return by_out<DT_FP8, EPI, 128, 1>(out_dt);
@@ -1203,54 +1201,42 @@ static const void* by_in(int in_dt, int out_dt) {
   return nullptr;
 }
 
-// 128-row tiles with the k-split wave layout (16-bit and fp8 inputs).
-template <int EPI>
-static const void* ksplit_by_in(int in_dt, int out_dt) {
-  switch (in_dt) {
-    case DT_F16: return by_out<DT_F16, EPI, 128, 2>(out_dt);
-    case DT_BF16: return by_out<DT_BF16, EPI, 128, 2>(out_dt);
-    case DT_FP8: return by_out<DT_FP8, EPI, 128, 2>(out_dt);
-  }
-  return nullptr;
-}
-
 // 256-row tiles: the split path with 16-bit or fp8 inputs.
 static const void* split256_by_in(int in_dt, int out_dt) {
   switch (in_dt) {
-    case DT_F16: return by_out<DT_F16, kEpiSplit, 256, 1>(out_dt);
-    case DT_BF16: return by_out<DT_BF16, kEpiSplit, 256, 1>(out_dt);
-    case DT_FP8: return by_out<DT_FP8, kEpiSplit, 256, 1>(out_dt);
+    case DT_F16: return by_out<DT_F16, kEpiSplit, 256, 0>(out_dt);
+    case DT_BF16: return by_out<DT_BF16, kEpiSplit, 256, 0>(out_dt);
+    case DT_FP8: return by_out<DT_FP8, kEpiSplit, 256, 0>(out_dt);
   }
   return nullptr;
 }
 
-// f32 logits (the unfused path's first kernel) on the 256-row and k-split
+// f32 logits (the unfused path's first kernel) on the 256-row and loader-wave
 // layouts, so that every tile variant also runs the unfused chain.
-template <int TM, int KS>
+template <int TM, int LW>
 static const void* logits_by_in(int in_dt) {
   switch (in_dt) {
-    case DT_F16: return tile_kernel_ptr<DT_F16, DT_F32, kEpiLogits, TM, KS>();
-    case DT_BF16: return tile_kernel_ptr<DT_BF16, DT_F32, kEpiLogits, TM, KS>();
-    case DT_FP8: return tile_kernel_ptr<DT_FP8, DT_F32, kEpiLogits, TM, KS>();
+    case DT_F16: return tile_kernel_ptr<DT_F16, DT_F32, kEpiLogits, TM, LW>();
+    case DT_BF16: return tile_kernel_ptr<DT_BF16, DT_F32, kEpiLogits, TM, LW>();
+    case DT_FP8: return tile_kernel_ptr<DT_FP8, DT_F32, kEpiLogits, TM, LW>();
   }
   return nullptr;
 }
 
-const void* chain_kernel_symbol(int in_dt, int out_dt, int epi, int tile_rows, int ks) {
+const void* chain_kernel_symbol(int in_dt, int out_dt, int epi, int tile_rows, int loaders) {
   if (tile_rows == 256) {
-    if (ks != 1) return nullptr;
+    if (loaders) return nullptr;
     if (epi == kEpiSplit) return split256_by_in(in_dt, out_dt);
-    if (epi == kEpiLogits) return out_dt == DT_F32 ? logits_by_in<256, 1>(in_dt) : nullptr;
+    if (epi == kEpiLogits) return out_dt == DT_F32 ? logits_by_in<256, 0>(in_dt) : nullptr;
     return nullptr;
   }
   if (tile_rows != 128) return nullptr;
-  if (ks == 2) {
-    if (epi == kEpiExchange) return ksplit_by_in<kEpiExchange>(in_dt, out_dt);
-    if (epi == kEpiSplit) return ksplit_by_in<kEpiSplit>(in_dt, out_dt);
-    if (epi == kEpiLogits) return out_dt == DT_F32 ? logits_by_in<128, 2>(in_dt) : nullptr;
+  if (loaders) {
+    if (epi == kEpiExchange) return loaders_by_in<kEpiExchange>(in_dt, out_dt);
+    if (epi == kEpiSplit) return loaders_by_in<kEpiSplit>(in_dt, out_dt);
+    if (epi == kEpiLogits) return out_dt == DT_F32 ? logits_by_in<128, 1>(in_dt) : nullptr;
     return nullptr;
   }
-  if (ks != 1) return nullptr;
   if (epi == kEpiExchange) return by_in<kEpiExchange>(in_dt, out_dt);
   if (epi == kEpiSplit) return by_in<kEpiSplit>(in_dt, out_dt);
   if (epi == kEpiLogits) return by_in<kEpiLogits>(in_dt, out_dt);
@@ -1268,12 +1254,12 @@ const void* rescale_kernel_symbol(int out_dt) {
 
 const void* zero_kernel_symbol() { return reinterpret_cast<const void*>(&zero_words_kernel); }
 
-template <int IN_DT, int KS>
+template <int IN_DT, int LW>
 static int lds_bytes_for(int out_dt) {
   switch (out_dt) {
-    case DT_F32: return EpiLayout<IN_DT, DT_F32, 128, KS, true>::TOTAL;
-    case DT_F16: return EpiLayout<IN_DT, DT_F16, 128, KS, true>::TOTAL;
-    case DT_BF16: return EpiLayout<IN_DT, DT_BF16, 128, KS, true>::TOTAL;
+    case DT_F32: return EpiLayout<IN_DT, DT_F32, 128, LW, true>::TOTAL;
+    case DT_F16: return EpiLayout<IN_DT, DT_F16, 128, LW, true>::TOTAL;
+    case DT_BF16: return EpiLayout<IN_DT, DT_BF16, 128, LW, true>::TOTAL;
   }
   return 0;
 }
@@ -1288,20 +1274,20 @@ int chain_kernel_threads(int in_dt) {
   return 0;
 }
 
-int chain_kernel_lds_bytes(int in_dt, int out_dt, int ks) {
-  if (ks == 2) {
+int chain_kernel_lds_bytes(int in_dt, int out_dt, int loaders) {
+  if (loaders) {
     switch (in_dt) {
-      case DT_F16: return lds_bytes_for<DT_F16, 2>(out_dt);
-      case DT_BF16: return lds_bytes_for<DT_BF16, 2>(out_dt);
-      case DT_FP8: return lds_bytes_for<DT_FP8, 2>(out_dt);
+      case DT_F16: return lds_bytes_for<DT_F16, 1>(out_dt);
+      case DT_BF16: return lds_bytes_for<DT_BF16, 1>(out_dt);
+      case DT_FP8: return lds_bytes_for<DT_FP8, 1>(out_dt);
     }
     return 0;
   }
   switch (in_dt) {
-    case DT_F32: return lds_bytes_for<DT_F32, 1>(out_dt);
-    case DT_F16: return lds_bytes_for<DT_F16, 1>(out_dt);
-    case DT_BF16: return lds_bytes_for<DT_BF16, 1>(out_dt);
-    case DT_FP8: return lds_bytes_for<DT_FP8, 1>(out_dt);
+    case DT_F32: return lds_bytes_for<DT_F32, 0>(out_dt);
+    case DT_F16: return lds_bytes_for<DT_F16, 0>(out_dt);
+    case DT_BF16: return lds_bytes_for<DT_BF16, 0>(out_dt);
+    case DT_FP8: return lds_bytes_for<DT_FP8, 0>(out_dt);
   }
   return 0;
 }

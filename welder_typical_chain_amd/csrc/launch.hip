@@ -41,8 +41,8 @@ int device_cu_count(int fallback) {
 // Dynamic LDS added to an exchange kernel (wave layout `ks`) so that no CU
 // holds two of its workgroups (spreads a grid of <= CU-count tiles over all
 // CUs).
-int exchange_lds_pad(int in_dt, int out_dt, int ks) {
-  const int stat = chain_kernel_lds_bytes(in_dt, out_dt, ks);
+int exchange_lds_pad(int in_dt, int out_dt, int loaders) {
+  const int stat = chain_kernel_lds_bytes(in_dt, out_dt, loaders);
   const int want = 80 * 1024 + 1024;
   return stat >= want ? 0 : want - stat;
 }
@@ -292,10 +292,10 @@ int device_state(int dev, DeviceState** out, bool host_objects = true) {
     for (int i = 0; i < 4; ++i)
       for (int o = 0; o < 3; ++o) {
         s.occ[i][o] = 1 << 30;
-        for (int ks = 1; ks <= 2; ++ks) {
-          const void* fn = chain_kernel_symbol(i, o, kEpiExchange, 128, ks);
-          if (!fn) continue;  // f32 has no k-split layout
-          const int pad = exchange_lds_pad(i, o, ks);
+        for (int lw = 0; lw <= 1; ++lw) {
+          const void* fn = chain_kernel_symbol(i, o, kEpiExchange, 128, lw);
+          if (!fn) continue;  // f32 has no loader-wave layout
+          const int pad = exchange_lds_pad(i, o, lw);
           HIP_TRY(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, pad));
           int nb = 0;
           HIP_TRY(hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, fn, chain_kernel_threads(i), pad));
@@ -388,7 +388,7 @@ struct TileKernel {
 };
 TileKernel tile_kernel(const VariantDesc& v, int in_dt, int out_dt, int epi) {
   if (v.id == kVarTile256x256) return {wide_kernel_symbol(in_dt, out_dt, epi), wide_kernel_threads()};
-  return {chain_kernel_symbol(in_dt, out_dt, epi, v.tile_rows, v.ks), chain_kernel_threads(in_dt)};
+  return {chain_kernel_symbol(in_dt, out_dt, epi, v.tile_rows, v.loaders), chain_kernel_threads(in_dt)};
 }
 
 // chain_tile_kernel: the scalars a tile needs before its first load lead the
@@ -821,9 +821,9 @@ int matmul_softmax_impl(const void* a, const void* b, void* out, int64_t batch, 
                         p, stream);
   }
   if (chosen == WTC_PATH_EXCHANGE)
-    return launch_exchange(ds, chain_kernel_symbol(in_dtype, out_dtype, kEpiExchange, 128, var.ks),
+    return launch_exchange(ds, chain_kernel_symbol(in_dtype, out_dtype, kEpiExchange, 128, var.loaders),
                            chain_kernel_threads(in_dtype), grid,
-                           exchange_lds_pad(in_dtype, out_dtype, var.ks), p, stream);
+                           exchange_lds_pad(in_dtype, out_dtype, var.loaders), p, stream);
   if (chosen == WTC_PATH_SPLIT) {
     const TileKernel tk = tile_kernel(var, in_dtype, out_dtype, kEpiSplit);
     rc = launch_tile(tk.fn, tk.threads, grid, 0, p, stream);

@@ -35,7 +35,7 @@ constexpr unsigned kSplitPaths = bit(WTC_PATH_SPLIT) | bit(WTC_PATH_UNFUSED);
 // The constants were fitted (least squares on the log of the time) to
 // back-to-back timings of every variant on every path over the 60 shapes
 // of calibrate.py on MI355X.  Fitted on three of its four shape sets and
-// scored on the fourth, in turn, the fused ranking lost 1.0 % on average
+// scored on the fourth, in turn, the fused ranking lost 0.84 % on average
 // against the measured fastest choice (the hand-written rules it replaces:
 // 5.3 %).
 struct TileCal {
@@ -43,26 +43,26 @@ struct TileCal {
   double fixed_cyc[3];  // per tile: exchange, split, logits epilogues
 };
 // [tile variant][0: 16-bit, 1: fp8, 2: f32]; fixed parts shared across input
-// types.  Rows: kVarTile128, kVarTile128KSplit, kVarTile256, kVarTile256x256.
+// types.  Rows: kVarTile128, kVarTile128Loaders, kVarTile256, kVarTile256x256.
 const TileCal kTileCal[4][3] = {
-    /* kVarTile128 */ {{658.4, {3754.4, 6262.6, 0}}, {580.1, {3754.4, 6262.6, 0}}, {4474.7, {3754.4, 6262.6, 0}}},
-    /* kVarTile128KSplit */ {{585.5, {4463.6, 7198.8, 1021}}, {530.4, {4463.6, 7198.8, 1021}}, {0, {0, 0, 0}}},
-    /* kVarTile256 */ {{1133.0, {0, 11531.6, 0}}, {1266.8, {0, 11531.6, 0}}, {0, {0, 0, 0}}},
-    /* kVarTile256x256 */ {{1949.5, {0, 22141.6, 5456}}, {1605.2, {0, 22141.6, 5456}}, {0, {0, 0, 0}}},
+    /* kVarTile128 */ {{635.87, {3678.9, 5946.6, 0}}, {617.19, {3678.9, 5946.6, 0}}, {4521.3, {3678.9, 5946.6, 0}}},
+    /* kVarTile128Loaders */ {{562.07, {4068.6, 6487.6, 254}}, {530.85, {4068.6, 6487.6, 254}}, {0, {0, 0, 0}}},
+    /* kVarTile256 */ {{1142.1, {0, 11628.2, 0}}, {1286.6, {0, 11628.2, 0}}, {0, {0, 0, 0}}},
+    /* kVarTile256x256 */ {{1973.6, {0, 20944.0, 6164}}, {1635.5, {0, 20944.0, 6164}}, {0, {0, 0, 0}}},
 };
 int cal_row(int id) { return id == kVarTile256x256 ? 3 : id; }
 // Rows kernel, cycles per row block: a fixed part, and per 128-column tile
 // (both passes) a fixed part and a part per 16-wide k-step.
-constexpr double kRowsBlockCyc = 1877.4, kRowsTileCyc = 4930.0, kRowsKstepCyc = 106.01;
+constexpr double kRowsBlockCyc = 1983.1, kRowsTileCyc = 4932.5, kRowsKstepCyc = 102.19;
 // Back-to-back launch cost of one kernel (us); the row exchange after the
 // last tile of a row block: fixed (us) and per column tile (us); the HBM
 // rate of the fused paths' streaming passes and the chip-wide rate that
 // prices k-tile bytes (GB/s).
-constexpr double kLaunchUs = 3.728, kExchangeUs = 0.3430, kExchangePerTileUs = 0.07890;
-constexpr double kHbmGBs = 7621.5, kFeedGBs = 75041.4;
+constexpr double kLaunchUs = 3.6597, kExchangeUs = 0.2592, kExchangePerTileUs = 0.08580;
+constexpr double kHbmGBs = 7919.8, kFeedGBs = 83312.1;
 // Unfused row passes (one 256-thread workgroup per row, eight per CU): HBM
 // rate, and the rate one workgroup streams its row at (GB/s).
-constexpr double kRowPassHbmGBs = 5280.0, kRowPassWgGBs = 5.582;
+constexpr double kRowPassHbmGBs = 5293.0, kRowPassWgGBs = 5.573;
 
 // Core clock under load, from the call's mean share of busy CUs: 1.5 GHz
 // with every CU busy throughout, ~2.1 with half of them or fewer (the chip's
@@ -83,18 +83,18 @@ static std::vector<VariantDesc> make_variants(int in_dt) {
   if (!valid_in(in_dt)) return v;
   const int64_t tk = 128 / in_bytes(in_dt);
   if (in_dt == WTC_DTYPE_F32) {
-    v.push_back({kVarTile128, "tile128x128_wave64x64", 128, 128, tk, 2, 32, 128, 1, kTilePaths});
+    v.push_back({kVarTile128, "tile128x128_wave64x64", 128, 128, tk, 2, 32, 128, 0, kTilePaths});
     return v;
   }
-  v.push_back({kVarTile128, "tile128x128_wave64x32", 128, 128, tk, 2, 16, 128, 1, kTilePaths});
-  v.push_back({kVarTile128KSplit, "tile128x128_wave64x64_ksplit2", 128, 128, tk, 2, 32, 128, 2,
+  v.push_back({kVarTile128, "tile128x128_wave64x32", 128, 128, tk, 2, 16, 128, 0, kTilePaths});
+  v.push_back({kVarTile128Loaders, "tile128x128_wave64x64_loaders", 128, 128, tk, 2, 32, 128, 1,
                kTilePaths});
-  v.push_back({kVarTile256, "tile256x128_wave64x64", 256, 128, tk, 2, 32, 256, 1, kSplitPaths});
+  v.push_back({kVarTile256, "tile256x128_wave64x64", 256, 128, tk, 2, 32, 256, 0, kSplitPaths});
   if (in_dt == WTC_DTYPE_F16 || in_dt == WTC_DTYPE_BF16)
-    v.push_back({kVarRows, "rows128_wave64x32_k128", 128, 128, kRowsMaxK, 2, 16, 128, 1,
+    v.push_back({kVarRows, "rows128_wave64x32_k128", 128, 128, kRowsMaxK, 2, 16, 128, 0,
                  bit(WTC_PATH_ROWS)});
   // tile_k: one 64-byte k-slab per ring stage
-  v.push_back({kVarTile256x256, "tile256x256_wave128x128", 256, 256, tk / 2, 4, 64, 256, 1,
+  v.push_back({kVarTile256x256, "tile256x256_wave128x128", 256, 256, tk / 2, 4, 64, 256, 0,
                kSplitPaths});
   return v;
 }

@@ -22,7 +22,7 @@ namespace wtc {
 
 enum VariantId : int {
   kVarTile128 = 0,        // 128x128 tile; 16-bit/fp8: 8 waves of 64x32, f32: 4 waves of 64x64
-  kVarTile128KSplit = 1,  // 128x128 tile, 8 waves of 64x64 in k-split pairs (16-bit/fp8)
+  kVarTile128Loaders = 1,  // 128x128 tile, 4 MFMA waves of 64x64 + 4 loader waves (16-bit/fp8)
   kVarTile256 = 2,        // 256x128 tile, 8 waves of 64x64 (16-bit/fp8)
   kVarRows = 3,           // one 128-row block over all of n, two passes (16-bit, k <= 128)
   kVarTile256x256 = 4,    // 256x256 tile, 4 waves of 128x128, 64-byte k-slabs (16-bit/fp8)
@@ -37,7 +37,7 @@ struct VariantDesc {
   const char* name;
   int64_t tile_m, tile_n, tile_k, thread_tile_m, thread_tile_n;
   int tile_rows;   // rows of one workgroup's tile (its columns: tile_n)
-  int ks;          // k-split factor of the wave layout
+  int loaders;     // 1: the 128-row layout whose loads are issued by loader waves
   unsigned paths;  // bit (1 << WTC_PATH_x) for each path the variant runs
 };
 

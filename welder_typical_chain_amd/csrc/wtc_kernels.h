@@ -36,16 +36,16 @@ struct ChainParams {
 };
 
 // tile_rows: 128, or 256 (split epilogue, and f32 logits, with 16-bit or fp8
-// inputs); ks: 1, or 2 for the k-split wave layout of 128-row tiles
+// inputs); loaders: 1 for the 128-row layout with 4 MFMA and 4 loader waves
 // (exchange and split epilogues, and f32 logits, with 16-bit or fp8 inputs).
 // NULL for a combination not built.
-const void* chain_kernel_symbol(int in_dt, int out_dt, int epi, int tile_rows = 128, int ks = 1);
+const void* chain_kernel_symbol(int in_dt, int out_dt, int epi, int tile_rows = 128, int loaders = 0);
 const void* rescale_kernel_symbol(int out_dt);
 // Waves that share one row in rescale_rows_kernel (its grid is rows * wpr / 4).
 int rescale_waves_per_row(int64_t rows_total, int cu_count);
 const void* zero_kernel_symbol();
 // Static LDS of the exchange-epilogue kernel of this wave layout.
-int chain_kernel_lds_bytes(int in_dt, int out_dt, int ks = 1);
+int chain_kernel_lds_bytes(int in_dt, int out_dt, int loaders = 0);
 int chain_kernel_threads(int in_dt);  // workgroup size of chain_tile_kernel (every layout)
 
 // 256x256 tiles (wide_tile.hip): split epilogue (any output type) or f32
