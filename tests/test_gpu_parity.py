@@ -208,7 +208,8 @@ def test_exchange_calls_on_two_streams(native_lib):
 @needs_gpu
 @pytest.mark.parametrize("in_dtype,out_dtype", [("f16", "f16"), ("bf16", "bf16"), ("f16", "f32"),
                                                 ("bf16", "f16")])
-@pytest.mark.parametrize("m,n,k", [(200, 264, 72), (128, 128, 128), (64, 4104, 8), (300, 136, 120)])
+@pytest.mark.parametrize("m,n,k", [(200, 264, 72), (128, 128, 128), (64, 4104, 8), (300, 136, 120),
+                                   (128, 384, 128), (300, 520, 120)])
 def test_rows_path_shapes(native_lib, in_dtype, out_dtype, m, n, k):
     """The one-workgroup-per-row-block path: ragged M / N, K below the
     k-step, a wide row of many column tiles."""
@@ -217,6 +218,23 @@ def test_rows_path_shapes(native_lib, in_dtype, out_dtype, m, n, k):
     inp = O.make_inputs(cfg, seed=5)
     out = run_chain(inp, in_dtype, out_dtype, path="rows")
     _check(cfg, inp, out, np.arange(m))
+
+
+@needs_gpu
+@pytest.mark.parametrize("m,n,k", [(66560 - 37, 392, 72), (128000, 384, 128), (179200 - 100, 264, 64)])
+def test_rows_path_many_row_blocks(native_lib, m, n, k):
+    """520 to 1400 row blocks of one batch (two to six workgroups per CU, in
+    waves), ragged rows and columns, against the oracle on sampled rows."""
+    from welder_typical_chain_amd import _lib
+    cu = torch.cuda.get_device_properties(0).multi_processor_count
+    pl = _lib.plan(1, m, n, k, 1, 1, _lib.PATH_ROWS, None, cu)
+    assert pl["grid"] == -(-m // 128), pl
+    cfg = ChainConfig("rows-many", 1, m, n, k, "f16", "f16", "normal", 0.4, logit_scale=0.7)
+    _announce(f"rows path, {m}x{n}x{k}")
+    inp = O.make_inputs(cfg, seed=13)
+    out = run_chain(inp, "f16", "f16", path="rows")
+    rows = np.unique(np.concatenate([sample_rows(m, 12, seed=k), np.arange(0, m, 2431), [m - 1]]))
+    _check(cfg, inp, out, rows)
 
 
 @needs_gpu
