@@ -116,22 +116,21 @@ chain_rows_kernel(const ChainParams p) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) rbv[i] = __builtin_amdgcn_readfirstlane(r[i]);
   }
-  uint32_t boff[BPW], bcol[BPW];
-#pragma unroll
-  for (int q = 0; q < BPW; ++q) {
-    const int blk = dma_block(wave_u, q, BPW);
-    const uint32_t krow = (uint32_t)dma_b_row(blk, lane);
-    bcol[q] = 8u * (uint32_t)dma_b_chunk(blk, lane);
-    boff[q] = krow < K ? krow * ldb + bcol[q] * 2 : kOutOfRange;
-  }
+  // A lane's k-row is krow0 + 4q for its load q, and its column group does
+  // not depend on q.  k-rows past K are clamped to K, whose offset lies past
+  // the buffer descriptor (one batch slice of B, < 2 GiB): they read zero.
+  const uint32_t krow0 = (uint32_t)dma_b_row(dma_block(wave_u, 0, BPW), lane);
+  const uint32_t bcol = 8u * (uint32_t)dma_b_chunk(dma_block(wave_u, 0, BPW), lane);
   const uint32_t lds0 = (uint32_t)(uintptr_t)(WTC_LDS uint8_t*)smem + RING_OFF;
   const int total = 2 * nT;
-  // Tile `it` of the 2*nT-tile stream (pass 1 then pass 2) into its stage.
+  // Tile `it` of the 2*nT-tile stream (pass 1 then pass 2) into its stage;
+  // past the end of the stream (it < total + S) the loads read zero.
   auto issue_load = [&](int it, int q) {
-    const uint32_t j = (uint32_t)(it % nT);
-    const bool ok = it < total && boff[q] != kOutOfRange && j * BN + bcol[q] < N;
-    dma16(rbv, ok ? boff[q] + j * (BN * 2) : kOutOfRange,
-          lds0 + (it % S) * STAGE + dma_block(wave_u, q, BPW) * 1024);
+    int jt = it >= nT ? it - nT : it;
+    jt = jt >= nT ? jt - nT : jt;
+    const uint32_t col = (it < total ? (uint32_t)jt * BN : 0x40000000u) + bcol;
+    const uint32_t off = min(krow0 + 4u * (uint32_t)q, K) * ldb + col * 2;
+    dma16(rbv, col < N ? off : kOutOfRange, lds0 + (it % S) * STAGE + dma_block(wave_u, q, BPW) * 1024);
   };
   // B fragment of k-step s of the tile in stage `st`: columns nw .. nw+31.
   auto read_b = [&](const uint8_t* st, int s) {
@@ -239,10 +238,10 @@ chain_rows_kernel(const ChainParams p) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const uint32_t col = j * BN + nw + 8 * g + 4 * (lane >> 5);
-          const bool ok = row < M && col < N;
+          const uint32_t off = min(row, M) * ldo + col * 4;  // rows past M: past the descriptor
           __builtin_amdgcn_raw_buffer_store_b128(
               __builtin_bit_cast(u32x4, f32x4{po[4 * g], po[4 * g + 1], po[4 * g + 2], po[4 * g + 3]}),
-              ro, ok ? (int)(row * ldo + col * 4) : (int)kOutOfRange, 0, 0);
+              ro, col < N ? (int)off : (int)kOutOfRange, 0, 0);
         }
       } else {
         // trade halves with lane ^ 32 so each lane holds two 16-byte runs:
@@ -258,9 +257,9 @@ chain_rows_kernel(const ChainParams p) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
           const uint32_t col = c0 + 16u * h;
-          const bool ok = row < M && col < N;
+          const uint32_t off = min(row, M) * ldo + col * 2;  // rows past M: past the descriptor
           __builtin_amdgcn_raw_buffer_store_b128(h ? run1 : run0, ro,
-                                                 ok ? (int)(row * ldo + col * 2) : (int)kOutOfRange,
+                                                 col < N ? (int)off : (int)kOutOfRange,
                                                  0, 0);
         }
       }
