@@ -13,7 +13,8 @@ torch = pytest.importorskip("torch")
 from oracle import oracle as O  # noqa: E402
 from welder_typical_chain_amd.configs import CONFIGS, ChainConfig  # noqa: E402
 
-from .parity_util import check_row_sums, compare_rows, run_chain, sample_rows  # noqa: E402
+from .parity_util import (check_row_sums, compare_rows, logit_error_bound, run_chain,  # noqa: E402
+                          sample_rows)
 
 pytestmark = pytest.mark.gpu
 
@@ -32,8 +33,9 @@ def _check(cfg: ChainConfig, inp: O.ChainInputs, out: torch.Tensor, rows, batche
     metrics = []
     for bt in batches:
         logits, probs = O.chain_rows(inp.a[bt], inp.b[bt], rows, inp.scale)
+        err = logit_error_bound(inp.a[bt], inp.b[bt], rows, inp.scale, logits, cfg.in_dtype)
         metrics.append(compare_rows(out_np[bt][rows], probs, logits, cfg.out_dtype,
-                                    label=f"{cfg.name} batch {bt}", in_dtype=cfg.in_dtype))
+                                    label=f"{cfg.name} batch {bt}", in_dtype=cfg.in_dtype, logit_err=err))
     # the split path (also what "auto" picks for C4 and C5) rounds its output twice
     split = path == "split" or (path == "auto" and cfg.name in ("C4", "C5"))
     check_row_sums(out, cfg.name, roundings=2 if split else 1)
@@ -155,7 +157,9 @@ def test_c3_full_batch(native_lib):
     for bt in (0, 31, 63):
         logits, probs = O.chain_rows(inp.a[bt], inp.b[bt], rows, inp.scale)
         got = out[bt][torch.from_numpy(rows).to(out.device)].float().cpu().numpy()
-        compare_rows(got, probs, logits, cfg.out_dtype, label=f"C3 batch {bt}", in_dtype=cfg.in_dtype)
+        err = logit_error_bound(inp.a[bt], inp.b[bt], rows, inp.scale, logits, cfg.in_dtype)
+        compare_rows(got, probs, logits, cfg.out_dtype, label=f"C3 batch {bt}", in_dtype=cfg.in_dtype,
+                     logit_err=err)
     worst = 0.0
     for bt in range(0, 64, 8):  # row sums in chunks of 8 batches (16 Mi entries each)
         s = out[bt:bt + 8].float().sum(-1)

@@ -20,7 +20,7 @@ torch = pytest.importorskip("torch")
 from oracle import oracle as O  # noqa: E402
 from welder_typical_chain_amd.configs import ChainConfig  # noqa: E402
 
-from .parity_util import check_row_sums, compare_rows, run_chain  # noqa: E402
+from .parity_util import check_row_sums, compare_rows, logit_error_bound, run_chain  # noqa: E402
 
 pytestmark = pytest.mark.gpu
 
@@ -82,8 +82,9 @@ def test_variant_parity(native_lib, in_dtype, out_dtype, variant, tiles, path, s
     rows = np.arange(m)
     for bt in range(batch):
         logits, probs = O.chain_rows(inp.a[bt], inp.b[bt], rows, inp.scale)
+        err = logit_error_bound(inp.a[bt], inp.b[bt], rows, inp.scale, logits, in_dtype)
         compare_rows(out_np[bt], probs, logits, out_dtype, label=f"{variant} {path} batch {bt}",
-                     in_dtype=in_dtype)
+                     in_dtype=in_dtype, logit_err=err)
     check_row_sums(out, f"{variant} {path}", roundings=2 if path == "split" else 1)
 
 
