@@ -20,7 +20,11 @@
  * must be a multiple of 16 and n a multiple of 8.  m, n, batch may be 0
  * (nothing to do); k may be 0 (every row is uniform 1/n).
  *
- * Thread safety: calls may come from any host thread.  Calls that share a
+ * Thread safety: calls may come from any host thread.  One lock per process
+ * covers the library's shared state (plans, default workspaces, the timeout
+ * mailbox) and is released before the ROWS, SPLIT and UNFUSED launches, so
+ * such calls from several threads enqueue in parallel; EXCHANGE-path calls
+ * hold it through their launch (see below).  Calls that share a
  * caller workspace must not overlap on the GPU (the default workspaces are
  * per stream, so NULL-workspace calls on different streams never share one).
  * An EXCHANGE-path call needs all of its tiles resident at once: the library

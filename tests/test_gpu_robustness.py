@@ -8,6 +8,8 @@
 * Default workspaces: one per stream, grow-only; none is allocated while the
   stream is being captured; a graph captured with the default workspace still
   replays correctly after an eager call of a larger shape grew it.
+* Calls from several host threads at once, each on its own stream, give the
+  one-thread results.
 """
 from __future__ import annotations
 
@@ -62,9 +64,17 @@ def test_exchange_timeout_is_reported(native_lib):
         assert reported and flags & 1 and timeouts > 0
         # reported once: the status is clean now
         check_status()
-        # a timeout left in the mailbox is reported by the next call, which does nothing else
-        matmul_softmax(a, b, path="exchange", workspace=ws)
-        torch.cuda.synchronize()
+        # a timeout left in the mailbox is reported by the next call, which does nothing else.
+        # Whether a call times out at this limit depends on the order the tiles start in, so
+        # calls are made until one has (its workspace counts the timed-out waits).
+        timed_out = False
+        for _ in range(8):
+            matmul_softmax(a, b, path="exchange", workspace=ws)
+            torch.cuda.synchronize()
+            if read_diagnostics(ws)[2] > 0:
+                timed_out = True
+                break
+        assert timed_out
         with pytest.raises(_lib.WtcError) as ei:
             matmul_softmax(a, b, path="exchange", workspace=ws)
         assert ei.value.code == _lib.WTC_ERR_TIMEOUT
@@ -130,3 +140,51 @@ def test_graph_with_default_workspace_survives_its_growth(native_lib):
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, ref), f"replay {rep}"
+
+
+@needs_gpu
+def test_calls_from_several_host_threads(native_lib):
+    """Four host threads, each with its own stream and workspace, call the
+    rows, split and unfused paths 8 times each at once (the launcher holds
+    its lock only for the shared state, not across these launches); every
+    output equals the one-thread result of the same call bit for bit."""
+    import threading
+
+    from welder_typical_chain_amd.chain import matmul_softmax, new_workspace, workspace_size
+
+    jobs = [("rows", 2, 300, 520, 64), ("split", 1, 256, 2048, 256), ("unfused", 1, 200, 264, 72)]
+    g = torch.Generator(device="cpu").manual_seed(11)
+    data = []
+    for path, batch, m, n, k in jobs:
+        a = (torch.randn(batch, m, k, generator=g) * 0.5).half().cuda()
+        b = (torch.randn(batch, k, n, generator=g) * 0.5).half().cuda()
+        ref = matmul_softmax(a, b, path=path)
+        data.append((path, a, b, ref, workspace_size(batch, m, n, k, 1, 1, path)))
+    torch.cuda.synchronize()
+    errors = []
+
+    def worker(tid):
+        try:
+            stream = torch.cuda.Stream()
+            with torch.cuda.stream(stream):
+                wss = [new_workspace(nb, torch.device("cuda")) for *_, nb in data]
+                outs = []
+                for _ in range(8):
+                    for (path, a, b, _, _), ws in zip(data, wss):
+                        outs.append((path, matmul_softmax(a, b, path=path, workspace=ws)))
+            stream.synchronize()
+            for i, (path, o) in enumerate(outs):
+                ref = data[i % len(data)][3]
+                if not torch.equal(o, ref):
+                    errors.append(f"thread {tid} call {i} ({path}) differs")
+        except Exception as e:  # noqa: BLE001 - reported below
+            errors.append(f"thread {tid}: {e!r}")
+
+    print("\n[gpu-case] 4 host threads x 24 calls (rows, split, unfused)", flush=True)
+    threads = [threading.Thread(target=worker, args=(t,)) for t in range(4)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=60)
+    assert not any(t.is_alive() for t in threads), "a host thread did not finish"
+    assert not errors, errors[:4]

@@ -743,7 +743,11 @@ int matmul_softmax_impl(const void* a, const void* b, void* out, int64_t batch, 
 
   int dev = 0;
   HIP_TRY(hipGetDevice(&dev));
-  std::lock_guard<std::mutex> lk(g_mu);
+  // The lock covers the shared state (device state, plan cache, default
+  // workspaces, mailbox, the exchange path's cross-stream event); the
+  // launches of the other paths only read this call's own values, so they
+  // run unlocked and calls from several host threads enqueue in parallel.
+  std::unique_lock<std::mutex> lk(g_mu);
   DeviceState* ds = nullptr;
   rc = device_state(dev, &ds, !noalloc);
   if (rc) return rc;
@@ -816,6 +820,8 @@ int matmul_softmax_impl(const void* a, const void* b, void* out, int64_t batch, 
   p.mailbox = ds->mailbox_dev;
   p.spin_ticks = g_spin_ticks.load();
 
+  const int cu_count = ds->cu_count;
+  if (chosen != WTC_PATH_EXCHANGE) lk.unlock();
   if (chosen == WTC_PATH_ROWS) {
     return launch_chain(rows_kernel_symbol(in_dtype, out_dtype), rows_kernel_threads(), grid, 0,
                         p, stream);
@@ -835,7 +841,7 @@ int matmul_softmax_impl(const void* a, const void* b, void* out, int64_t batch, 
             ldo = p.ldo_bytes, ob = p.o_bstride;
     int nT = p.nT;
     int tshift = var.tile_n == 256 ? 8 : 7;  // log2 of the tile width
-    int wpr = rescale_waves_per_row(rows_total, ds->cu_count);
+    int wpr = rescale_waves_per_row(rows_total, cu_count);
     void* args[] = {&o, &part, &rows_total, &M_, &rows_pad, &N_, &ldo, &ob, &nT, &tshift, &wpr};
     HIP_TRY(hipLaunchKernel(rescale_kernel_symbol(out_dtype),
                             dim3((unsigned)ceil_div(rows_total * wpr, kRescaleRowsPerWg)), dim3(256),
