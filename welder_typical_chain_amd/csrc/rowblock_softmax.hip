@@ -245,14 +245,17 @@ chain_rows_kernel(const ChainParams p) {
         }
       } else {
         // trade halves with lane ^ 32 so each lane holds two 16-byte runs:
-        // l < 32 columns 0-7 and 16-23, l >= 32 columns 8-15 and 24-31
+        // l < 32 columns 0-7 and 16-23, l >= 32 columns 8-15 and 24-31.
+        // v_permlane32_swap(x, y) leaves {x[0..31], y[0..31]} in x and
+        // {x[32..63], y[32..63]} in y, so one swap of words w and w + 2
+        // yields words w and w + 2 of the run in every lane, in registers.
         const bool lo = lane < 32;
-        const uint32_t s0 = lo ? pw[2] : pw[0], s1 = lo ? pw[3] : pw[1];
-        const uint32_t s2 = lo ? pw[6] : pw[4], s3 = lo ? pw[7] : pw[5];
-        const uint32_t r0 = __shfl_xor(s0, 32), r1 = __shfl_xor(s1, 32);
-        const uint32_t r2 = __shfl_xor(s2, 32), r3 = __shfl_xor(s3, 32);
-        const u32x4 run0 = lo ? u32x4{pw[0], pw[1], r0, r1} : u32x4{r0, r1, pw[2], pw[3]};
-        const u32x4 run1 = lo ? u32x4{pw[4], pw[5], r2, r3} : u32x4{r2, r3, pw[6], pw[7]};
+        const auto q0 = __builtin_amdgcn_permlane32_swap(pw[0], pw[2], false, false);
+        const auto q1 = __builtin_amdgcn_permlane32_swap(pw[1], pw[3], false, false);
+        const auto q2 = __builtin_amdgcn_permlane32_swap(pw[4], pw[6], false, false);
+        const auto q3 = __builtin_amdgcn_permlane32_swap(pw[5], pw[7], false, false);
+        const u32x4 run0 = u32x4{q0[0], q1[0], q0[1], q1[1]};
+        const u32x4 run1 = u32x4{q2[0], q3[0], q2[1], q3[1]};
         const uint32_t c0 = j * BN + nw + (lo ? 0u : 8u);
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
