@@ -82,22 +82,43 @@ __device__ inline u32x2 tr_read(const uint8_t* p) {
 }
 
 // -------------------------------------------------------------------------
-// Output conversion: four f32 -> two 32-bit words of f16 / bf16 (RNE)
+// Output conversion: four f32 -> two 32-bit words of f16 / bf16 (RNE).  A
+// two-element vector conversion selects gfx950's packed converts
+// (v_cvt_pk_f16_f32 / v_cvt_pk_bf16_f32: one instruction per word instead
+// of two converts and an or); the whole vector is bit cast, never an element.
 // -------------------------------------------------------------------------
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 template <int OUT_DT> __device__ inline void pack4(const f32x4& x, uint32_t* w0, uint32_t* w1);
 template <> __device__ inline void pack4<DT_F16>(const f32x4& x, uint32_t* w0, uint32_t* w1) {
-  const float x0 = x[0], x1 = x[1], x2 = x[2], x3 = x[3];
+  const f16x2 lo = __builtin_convertvector(f32x2{x[0], x[1]}, f16x2);
+  const f16x2 hi = __builtin_convertvector(f32x2{x[2], x[3]}, f16x2);
+  *w0 = __builtin_bit_cast(uint32_t, lo);
+  *w1 = __builtin_bit_cast(uint32_t, hi);
+}
+template <> __device__ inline void pack4<DT_BF16>(const f32x4& x, uint32_t* w0, uint32_t* w1) {
+  const bf16x2 lo = __builtin_convertvector(f32x2{x[0], x[1]}, bf16x2);
+  const bf16x2 hi = __builtin_convertvector(f32x2{x[2], x[3]}, bf16x2);
+  *w0 = __builtin_bit_cast(uint32_t, lo);
+  *w1 = __builtin_bit_cast(uint32_t, hi);
+}
+
+// Four f32 values times f -> two words of the output type.  f16: scalar
+// conversions of the products, which the compiler fuses into v_fma_mixlo_f16
+// (one rounding of the exact product to f16, where a f32 multiply followed
+// by a packed convert would round twice); bf16: packed converts of the
+// products.
+template <int OUT_DT> __device__ inline void pack4_product(const f32x4& x, float f, uint32_t* w0, uint32_t* w1);
+template <> __device__ inline void pack4_product<DT_F16>(const f32x4& x, float f, uint32_t* w0, uint32_t* w1) {
+  const float x0 = x[0] * f, x1 = x[1] * f, x2 = x[2] * f, x3 = x[3] * f;
   *w0 = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x0) |
         ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x1) << 16);
   *w1 = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x2) |
         ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x3) << 16);
 }
-template <> __device__ inline void pack4<DT_BF16>(const f32x4& x, uint32_t* w0, uint32_t* w1) {
-  const float x0 = x[0], x1 = x[1], x2 = x[2], x3 = x[3];
-  *w0 = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x0) |
-        ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x1) << 16);
-  *w1 = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x2) |
-        ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x3) << 16);
+template <> __device__ inline void pack4_product<DT_BF16>(const f32x4& x, float f, uint32_t* w0, uint32_t* w1) {
+  pack4<DT_BF16>(x * f, w0, w1);
 }
 
 __device__ inline float wave_xor32_max(float x) { return fmaxf(x, __shfl_xor(x, 32)); }

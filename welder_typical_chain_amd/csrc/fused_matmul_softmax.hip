@@ -1049,14 +1049,13 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
     if (m < p.M && n < p.N) {
       const float f = EPI == kEpiLogits ? 1.0f : factor[(ch * EPC / (32 * NTN)) * BM + row];
       const float* src = stg + row * kStagePitch + ch * EPC;
-      const f32x4 x0 = *reinterpret_cast<const f32x4*>(src) * f;
       if constexpr (OSZ == 4) {
+        const f32x4 x0 = *reinterpret_cast<const f32x4*>(src) * f;
         store16(o_base + m * p.ldo_bytes + n * OSZ, __builtin_bit_cast(u32x4, x0));
       } else {
-        const f32x4 x1 = *reinterpret_cast<const f32x4*>(src + 4) * f;
         uint32_t w0, w1, w2, w3;
-        pack4<OUT_DT>(x0, &w0, &w1);
-        pack4<OUT_DT>(x1, &w2, &w3);
+        pack4_product<OUT_DT>(*reinterpret_cast<const f32x4*>(src), f, &w0, &w1);
+        pack4_product<OUT_DT>(*reinterpret_cast<const f32x4*>(src + 4), f, &w2, &w3);
         store16(o_base + m * p.ldo_bytes + n * OSZ, u32x4{w0, w1, w2, w3});
       }
     }
