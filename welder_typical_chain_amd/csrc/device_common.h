@@ -132,6 +132,34 @@ __device__ inline float dpp_quad(float x) {
 }
 __device__ inline float wave_xor32_sum(float x) { return x + __shfl_xor(x, 32); }
 
+// The same reductions with the lane 32 apart in registers: v_permlane32_swap
+// of x with itself leaves x[l % 32] in word 0 and x[l % 32 + 32] in word 1
+// of every lane l, so both halves combine the pair in the same operand
+// order (bit-identical results) without an LDS round trip.  The words are
+// copied to scalars before the bit cast.
+__device__ inline void xor32_pair(float x, float* lo, float* hi) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const auto q = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  const uint32_t a = q[0], b = q[1];
+  *lo = __builtin_bit_cast(float, a);
+  *hi = __builtin_bit_cast(float, b);
+}
+__device__ inline float xor32_max(float x) {
+  float a, b;
+  xor32_pair(x, &a, &b);
+  return fmaxf(a, b);
+}
+__device__ inline float xor32_min(float x) {
+  float a, b;
+  xor32_pair(x, &a, &b);
+  return fminf(a, b);
+}
+__device__ inline float xor32_sum(float x) {
+  float a, b;
+  xor32_pair(x, &a, &b);
+  return a + b;
+}
+
 // 64-bit relaxed atomic access at agent scope for the split path's per-tile
 // row statistics (max, sumexp): one store, so a reader never sees half of it.
 __device__ inline void store_stat(float2* p, float m, float s) {

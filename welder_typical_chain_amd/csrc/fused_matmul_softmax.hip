@@ -794,6 +794,12 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
   // the final scale factors are combined from those, so one LDS exchange
   // serves both.  Loader waves (LW = 1) hold no block: they skip the
   // per-wave statistics and the staging and take part in the rest.
+  //
+  // The statistics run on the raw accumulators: y = c2 * acc (log2 domain)
+  // is monotone in acc, so a row's max of y is c2 times its max of acc (its
+  // min when c2 < 0; rounding is monotone, so this is exactly the max of the
+  // rounded products), and each exponential is exp2(fma(acc, c2, -max)),
+  // one instruction before the exponent and one rounding of its argument.
   const int jr = acc_j(lane);
   const int nvalid = p.N - n0 < BN ? (int)(p.N - n0) : BN;  // columns of this tile inside N
   if constexpr (EPI == kEpiLogits) {
@@ -804,15 +810,15 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[mt][j][v] *= p.lin_scale;
   } else {
-    // y = c2 * acc (log2 domain); columns past N get -inf (ragged last tile only)
-    if (nvalid == BN) {
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-        for (int j = 0; j < NTN; ++j)
-#pragma unroll
-          for (int v = 0; v < 16; ++v) acc[mt][j][v] *= p.c2;
-    } else {
+    float c2 = p.c2;
+    if (nvalid < BN) {
+      // Ragged last column tile: columns past N get the accumulator value
+      // that no max (min) selects and whose exponential is 0: -inf, or +inf
+      // when c2 < 0.  A zero scale makes every logit 0: the columns inside N
+      // get 0 and the scale 1, so the padding still works.
+      if (c2 == 0.0f) c2 = 1.0f;
+      const float pad = c2 < 0.0f ? INFINITY : -INFINITY;
+      const bool zero = p.c2 == 0.0f;
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
@@ -820,28 +826,41 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
 #pragma unroll
           for (int v = 0; v < 16; ++v) {
             const int n_loc = nw + j * 32 + acc_i(lane, v);
-            acc[mt][j][v] = n_loc < nvalid ? acc[mt][j][v] * p.c2 : -INFINITY;
+            acc[mt][j][v] = n_loc < nvalid ? (zero ? 0.0f : acc[mt][j][v]) : pad;
           }
     }
+    const bool neg = c2 < 0.0f;  // wave-uniform
 #pragma unroll
     for (int mt = 0; mt < (loader ? 0 : 2); ++mt) {
-      float mx = -INFINITY;
+      // the row's extreme accumulator over the wave's columns (lane l and
+      // l ^ 32 hold the two halves of the row)
+      float ext = acc[mt][0][0];
+      if (neg) {
 #pragma unroll
-      for (int j = 0; j < NTN; ++j)
+        for (int j = 0; j < NTN; ++j)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) mx = fmaxf(mx, acc[mt][j][v]);
-      mx = wave_xor32_max(mx);
-      const float base = mx == -INFINITY ? 0.0f : mx;  // every column of this wave past N
-      float sm = 0.0f;
+          for (int v = 0; v < 16; ++v) ext = fminf(ext, acc[mt][j][v]);
+        ext = xor32_min(ext);
+      } else {
+#pragma unroll
+        for (int j = 0; j < NTN; ++j)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) ext = fmaxf(ext, acc[mt][j][v]);
+        ext = xor32_max(ext);
+      }
+      // max of y; -inf when every column of the wave lies past N (pad * c2)
+      const float mx = ext * c2;
+      const float nbase = mx == -INFINITY ? 0.0f : -mx;
+      float s4[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // independent partial sums
 #pragma unroll
       for (int j = 0; j < NTN; ++j)
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-          const float e = __builtin_amdgcn_exp2f(acc[mt][j][v] - base);
+          const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[mt][j][v], c2, nbase));
           acc[mt][j][v] = e;
-          sm += e;
+          s4[v & 3] += e;
         }
-      sm = wave_xor32_sum(sm);
+      const float sm = xor32_sum((s4[0] + s4[1]) + (s4[2] + s4[3]));
       if (lane < 32) wstat[wn * BM + wm * 64 + mt * 32 + jr] = make_float2(mx, sm);
     }
   }
@@ -864,10 +883,11 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
   // A row block of a single column tile (N <= 128) needs no exchange: the
   // tile's own statistics are the row's.
   const bool solo = EPI == kEpiExchange && nT32 == 1u;
-  // Exchange path: the row's log-sum-exp over this tile (log2 domain) per
-  // tile row, and the generation words of the row block's slots, in LDS.
-  float* tlse = factor + WN * BM;                             // [BM]
-  uint32_t* sgen = reinterpret_cast<uint32_t*>(tlse + BM);    // [64]
+  // Exchange path: the generation words of the row block's slots in LDS, and
+  // the table of the row block's per-tile log-sum-exps [slot][kLsePitch]
+  // (log2 domain; this tile's own slot is filled from its statistics).
+  uint32_t* sgen = reinterpret_cast<uint32_t*>(factor + WN * BM + BM);  // [64]
+  float* lse_all = reinterpret_cast<float*>(smem + L::LSE_OFF);
   const uint32_t own_slot = slot0 + nt;
   if constexpr (EPI == kEpiExchange)
     if (t < 64 && (uint32_t)t < nT32) sgen[t] = gen_lane;
@@ -878,7 +898,7 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
       if constexpr (EPI == kEpiExchange) {
         // publish the row's log-sum-exp over this tile with this launch's tag
         const float lse = st.x + __builtin_amdgcn_logf(st.y);
-        tlse[t] = lse;
+        lse_all[nt * kLsePitch + t] = lse;
         if (!solo) store_entry(p.ent + (uint64_t)own_slot * BM + t, lse, sgen[nt] + 1u);
         // Wait until the entry stores are acknowledged.  Not for ordering --
         // the tags make every entry self-describing -- but measured: without
@@ -893,28 +913,102 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
   }
 
   // Stage the tile in LDS as f32 (the ring is free: every load has landed
-  // and every wave is past the last k-tile).  This overlaps the entry stores
-  // and, on the exchange path, precedes the wait for the other tiles.
+  // and every wave is past the last k-tile), for the stores' 16-byte rows.
   float* stg = reinterpret_cast<float*>(smem);
+  auto stage_tile = [&]() {
 #pragma unroll
-  for (int mt = 0; mt < (loader ? 0 : 2); ++mt)
+    for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-    for (int j = 0; j < NTN; ++j)
+      for (int j = 0; j < NTN; ++j)
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int m_loc = wm * 64 + mt * 32 + jr;
-        const int n_loc = nw + j * 32 + acc_i(lane, 4 * g);
-        *reinterpret_cast<f32x4*>(stg + m_loc * kStagePitch + n_loc) =
-            f32x4{acc[mt][j][4 * g], acc[mt][j][4 * g + 1], acc[mt][j][4 * g + 2],
-                  acc[mt][j][4 * g + 3]};
+        for (int g = 0; g < 4; ++g) {
+          const int m_loc = wm * 64 + mt * 32 + jr;
+          const int n_loc = nw + j * 32 + acc_i(lane, 4 * g);
+          *reinterpret_cast<f32x4*>(stg + m_loc * kStagePitch + n_loc) =
+              f32x4{acc[mt][j][4 * g], acc[mt][j][4 * g + 1], acc[mt][j][4 * g + 2],
+                    acc[mt][j][4 * g + 3]};
+        }
+  };
+
+  // Exchange path: poll the other tiles' half-slots of the row block into
+  // the table.  Polling wave pw of NWP takes half-slots hs = pw, pw + NWP,
+  // ... (slot hs / 2, rows (hs % 2) * 64 + lane), U at a time: one wave load
+  // is 64 consecutive rows of one slot (512 contiguous bytes), and a
+  // half-slot is done when every lane's entry carries the expected tag;
+  // otherwise the wave sleeps briefly and reloads only what is not done.
+  auto poll_table = [&](int pw_any, int NWP) {
+    constexpr int U = 8;
+    const int pw = __builtin_amdgcn_readfirstlane(pw_any);  // wave-uniform: scalar branches
+    const int nT = (int)nT32;
+    bool in_time = true;
+    uint64_t waited = 0;
+    for (int hb = pw; hb < 2 * nT; hb += U * NWP) {
+      bool done[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int hs = hb + NWP * u;
+        done[u] = !(hs < 2 * nT && (hs >> 1) != (int)nt);  // wave-uniform
       }
+      const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+      for (;;) {
+        uint64_t e[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int hs = hb + NWP * u;
+          if (!done[u])
+            e[u] = load_entry(p.ent + (uint64_t)(slot0 + (hs >> 1)) * BM + (hs & 1) * 64 + lane);
+        }
+        bool all = true;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int hs = hb + NWP * u, q = hs >> 1;
+          if (!done[u]) {
+            if (__all(entry_tag(e[u]) == sgen[q] + 1u) || !in_time) {
+              done[u] = true;
+              lse_all[q * kLsePitch + (hs & 1) * 64 + lane] = entry_lse(e[u]);
+            } else {
+              all = false;
+            }
+          }
+        }
+        if (all) break;
+        __builtin_amdgcn_s_sleep(1);
+        const uint64_t w = __builtin_amdgcn_s_memrealtime() - t0;
+        waited = w > waited ? w : waited;
+        if (w > p.spin_ticks) in_time = false;  // one more pass takes what is there
+      }
+    }
+    if (lane == 0 && waited > 0) {
+      record_wait(p.err, waited);
+      if (!in_time) report_timeout(p.err, p.mailbox);
+    }
+  };
+
+  if constexpr (EPI == kEpiExchange && LDW) {
+    // Loader waves poll as soon as this tile's entries are acknowledged,
+    // while the MFMA waves stage the tile.
+    __syncthreads();  // this tile's entry stores are acknowledged
+    if (!loader)
+      stage_tile();
+    else if (!solo)
+      poll_table(wave - C::kMfmaWaves, C::kWaves - C::kMfmaWaves);
+    __syncthreads();  // the table and the staged tile are complete
+  } else {
+    if (!loader) stage_tile();
+    if constexpr (EPI == kEpiExchange) {
+      __syncthreads();  // the entries are acknowledged, the own log-sum-exps in the table
+      if (!solo) {
+        poll_table(wave, NT / 64);
+        __syncthreads();  // the table is complete
+      }
+    }
+  }
 
   if constexpr (EPI != kEpiLogits) {
     constexpr int P = NT / BM;  // threads per row (WN, or 2 WN with loader waves)
     static_assert(P % WN == 0 && (P & (P - 1)) == 0 && P <= 4, "threads per row");
     const int r = t / P, h = t % P;
     if constexpr (EPI == kEpiExchange) {
-      __syncthreads();  // tlse and sgen are in place
       float gm = -INFINITY, gs = 0.0f;  // running max and sum of exp2(L - gm)
       if (solo) {
         if (h == 0) {  // the row's statistics from this tile's wave entries in LDS
@@ -923,90 +1017,43 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
           gs = ts.y;
         }
       } else {
-        // Wave w polls half-slots hs = w, w + NW, w + 2 NW, ... (slot hs / 2,
-        // rows (hs % 2) * 64 + lane), four at a time, and puts the
-        // log-sum-exps in the LDS table.  This tile's own slot comes from tlse.
-        constexpr int NW = NT / 64;  // waves
+        // Thread h of the row's P merges the tile log-sum-exps q = h, h + P,
+        // h + 2P, ... in groups of four: every read is unconditional (an index
+        // past nT reads slot 0 and is replaced by -inf), so the four reads
+        // issue together.
         const int nT = (int)nT32;
-        float* lse_all = reinterpret_cast<float*>(smem + L::LSE_OFF);  // [slot][kLsePitch]
-        bool in_time = true;
-        uint64_t waited = 0;
-        for (int hb = wave; hb < 2 * nT; hb += 4 * NW) {
-          bool done[4];
-#pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            const int hs = hb + NW * u;
-            done[u] = !(hs < 2 * nT && (hs >> 1) != (int)nt);  // wave-uniform
-          }
-          const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-          for (;;) {
-            uint64_t e[4];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-              const int hs = hb + NW * u;
-              if (!done[u])
-                e[u] = load_entry(p.ent + (uint64_t)(slot0 + (hs >> 1)) * BM + (hs & 1) * 64 + lane);
-            }
-            bool all = true;
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-              const int hs = hb + NW * u, q = hs >> 1;
-              if (!done[u]) {
-                if (__all(entry_tag(e[u]) == sgen[q] + 1u) || !in_time) {
-                  done[u] = true;
-                  lse_all[q * kLsePitch + (hs & 1) * 64 + lane] = entry_lse(e[u]);
-                } else {
-                  all = false;
-                }
-              }
-            }
-            if (all) break;
-            __builtin_amdgcn_s_sleep(1);
-            const uint64_t w = __builtin_amdgcn_s_memrealtime() - t0;
-            waited = w > waited ? w : waited;
-            if (w > p.spin_ticks) in_time = false;  // one more pass takes what is there
-          }
-        }
-        if (lane == 0 && waited > 0) {
-          record_wait(p.err, waited);
-          if (!in_time) report_timeout(p.err, p.mailbox);
-        }
-        __syncthreads();  // the table is complete
-        // The P threads of a row each merge a share of its nT tile
-        // log-sum-exps, then combine with their partner lanes.
-        const int part = (nT + P - 1) / P;
-        const int q0 = h * part < nT ? h * part : nT;
-        const int q1 = q0 + part < nT ? q0 + part : nT;
-        for (int qb = q0; qb < q1; qb += 4) {  // four independent table reads at a time
+        const int ng = (nT + 4 * P - 1) / (4 * P);
+        for (int g = 0; g < ng; ++g) {
           float l[4];
 #pragma unroll
           for (int u = 0; u < 4; ++u) {
-            const int q = qb + u;
-            l[u] = q >= q1 ? -INFINITY : (q == (int)nt ? tlse[r] : lse_all[q * kLsePitch + r]);
+            const int q = g * 4 * P + u * P + h;
+            const float v = lse_all[(q < nT ? q : 0) * kLsePitch + r];
+            l[u] = q < nT ? v : -INFINITY;
           }
-          const float nm = fmaxf(gm, fmaxf(fmaxf(l[0], l[1]), fmaxf(l[2], l[3])));  // finite
-          float cs = gm == -INFINITY ? 0.0f : gs * __builtin_amdgcn_exp2f(gm - nm);
+          const float nm = fmaxf(gm, fmaxf(fmaxf(l[0], l[1]), fmaxf(l[2], l[3])));
+          const float ref = nm == -INFINITY ? 0.0f : nm;  // no entry at all in this share
+          float cs = gm == -INFINITY ? 0.0f : gs * __builtin_amdgcn_exp2f(gm - ref);
 #pragma unroll
-          for (int u = 0; u < 4; ++u) cs += __builtin_amdgcn_exp2f(l[u] - nm);
+          for (int u = 0; u < 4; ++u) cs += __builtin_amdgcn_exp2f(l[u] - ref);
           gm = nm;
           gs = cs;
         }
       }
-      // The P threads of row r are P consecutive lanes of one quad: combine
-      // with DPP quad permutes (xor 1, then xor 2).  gm == -inf only for an
-      // empty share; its sum is 0.
+      // The P threads of row r are P consecutive lanes of one quad: the row
+      // max over the quad (DPP quad permutes xor 1, xor 2), each share
+      // rescaled to it, then the sum over the quad.  Some share holds a
+      // finite log-sum-exp (every tile has a column inside N), so M is finite;
+      // a share without entries has gm = -inf and contributes 0.
+      float M = gm;
 #pragma unroll
-      for (int off = 1; off < P; off <<= 1) {
-        const float om = off == 1 ? dpp_quad<0xB1>(gm) : dpp_quad<0x4E>(gm);
-        const float os = off == 1 ? dpp_quad<0xB1>(gs) : dpp_quad<0x4E>(gs);
-        const float M = fmaxf(gm, om);
-        gs = (gm == -INFINITY ? 0.0f : gs * __builtin_amdgcn_exp2f(gm - M)) +
-             (om == -INFINITY ? 0.0f : os * __builtin_amdgcn_exp2f(om - M));
-        gm = M;
-      }
+      for (int off = 1; off < P; off <<= 1) M = fmaxf(M, off == 1 ? dpp_quad<0xB1>(M) : dpp_quad<0x4E>(M));
+      float S = gm == -INFINITY ? 0.0f : gs * __builtin_amdgcn_exp2f(gm - M);
+#pragma unroll
+      for (int off = 1; off < P; off <<= 1) S += off == 1 ? dpp_quad<0xB1>(S) : dpp_quad<0x4E>(S);
       // thread (r, h < WN) owns the factor of row r, column slice of wave h:
       // exp2(m_w - L) with L = max + log2(sum) the row's log-sum-exp
-      const float row_lse = gm + __builtin_amdgcn_logf(gs);
+      const float row_lse = M + __builtin_amdgcn_logf(S);
       if (h < WN) {
         const float mw = wstat[h * BM + r].x;
         factor[h * BM + r] = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - row_lse);
