@@ -8,11 +8,23 @@
  * Here "compiling" selects and plans the hand-written gfx950 kernel for the
  * chain (no code generation happens at run time): the chain is recognised
  * from the MLIR text, the tile parameters are checked against the kernel
- * variants the library is built with, and out_dir receives
- *   03.chain.canonical.mlir   the decomposed chain the kernel implements
+ * variants the library is built with, and out_dir receives, under the names
+ * the reference's header lists (WelderCompileCAPI.h:12-16) and its callers
+ * and scripts read:
+ *   03.after_postbufferize.mlir     the decomposed chain the kernel implements
+ *   04.after_workgroup_launch.mlir  one gpu.launch per HIP kernel: grid,
+ *                                   block, LDS as the workgroup(...) attribution
+ *   04c.after_linalg_to_loops.mlir  the loop structure of the path's kernels
+ *                                   (scf loops with this problem's bounds)
+ *   05.out.nvvm.runnable.mlir       the runnable module: one gpu.launch_func
+ *                                   per kernel of the gfx950 code object, with
+ *                                   the entry point and its arguments as
+ *                                   attributes (no NVVM is involved)
+ * and this build's own:
+ *   03.chain.canonical.mlir   the same chain as 03.after_postbufferize.mlir
  *   04.kernel.plan.json       kernel variant, path, grid / block / LDS
  *   05.out.hip.launch.json    the runnable artefact: library, C entry point
- *                             (wtc_matmul_softmax) and its arguments
+ *                             (wtc_matmul_softmax_tiles) and its arguments
  *   05.out.gfx950.hsaco       the gfx950 device code object of the chain
  *                             kernels (plus 05.out.rows.gfx950.hsaco for the
  *                             unfused path's row kernels)

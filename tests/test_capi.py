@@ -409,3 +409,17 @@ def test_compile_output_passes_reference_callers(L, tmp_path, name, fused):
         assert f"arith.constant {k['grid'][0]} : index" in launch
         assert f"arith.constant {k['block'][0]} : index" in launch
     assert f'wtc.path = "{plan_json["path"]}"' in runnable
+    # bench/pin_baseline.sh:44-51 copies 03 / 04 / 04c / 05 of both variants
+    # under `set -euo pipefail`: every one must exist
+    for name in ("03.after_postbufferize.mlir", "04.after_workgroup_launch.mlir",
+                 "04c.after_linalg_to_loops.mlir", "05.out.nvvm.runnable.mlir"):
+        assert (out / name).is_file() and (out / name).stat().st_size > 0, name
+    # bench/run_regression.sh:96-98,111-112 greps these patterns
+    assert re.search(r"workgroup\(", launch)
+    assert re.search(r"gpu\.launch_func", runnable)
+    assert runnable.count("gpu.launch_func") == len(plan_json["kernels"])
+    # 04c: one func per kernel, its grid as the parallel loop bound
+    loops = (out / "04c.after_linalg_to_loops.mlir").read_text()
+    assert loops.count("func.func @kernel") == len(plan_json["kernels"])
+    for k in plan_json["kernels"]:
+        assert f"%grid = arith.constant {k['grid'][0]} : index" in loops

@@ -124,7 +124,9 @@ def test_shipped_baseline_is_complete():
     for name in ("ab_summary.csv", "manifest.txt", "search/best.json"):
         assert (d / name).is_file(), name
     for variant in ("baseline", "fused"):
-        for name in ("03.chain.canonical.mlir", "04.kernel.plan.json", "05.out.hip.launch.json",
+        for name in ("03.after_postbufferize.mlir", "04.after_workgroup_launch.mlir",
+                     "04c.after_linalg_to_loops.mlir", "05.out.nvvm.runnable.mlir",
+                     "03.chain.canonical.mlir", "04.kernel.plan.json", "05.out.hip.launch.json",
                      "kernel_report.txt"):
             assert (d / variant / name).is_file(), (variant, name)
     assert PG.read_avg_ms(d / "ab_summary.tsv", "fused") < PG.read_avg_ms(d / "ab_summary.tsv", "baseline")
@@ -169,7 +171,8 @@ def test_pin_then_guard_on_gpu(native_lib, tmp_path):
     res = PB.pin(args, pinned)
     assert args.verify is False and res["verify"] == {}
     for name in ("ab_summary.tsv", "ab_summary.csv", "speedup.tsv", "manifest.txt",
-                 "search/best.json", "fused/05.out.hip.launch.json", "baseline/04.kernel.plan.json"):
+                 "search/best.json", "fused/05.out.hip.launch.json", "baseline/04.kernel.plan.json",
+                 "fused/04c.after_linalg_to_loops.mlir", "baseline/05.out.nvvm.runnable.mlir"):
         assert (pinned / name).is_file(), name
     manifest = dict(l.split("=", 1) for l in (pinned / "manifest.txt").read_text().splitlines())
     assert manifest["run_out_base"] == str(run_dir) and manifest["iters"] == "50"

@@ -102,6 +102,109 @@ static std::string memref_of(const ChainSpec& spec, int64_t d1, int64_t d2, Elem
   return o.str();
 }
 
+// One kernel of a path as the stage files describe it.
+struct StageKernel {
+  std::string name;   // display name (template arguments spelled out)
+  std::string kind;   // tile_exchange / tile_split / tile_logits / rows / rescale / rowmax / ...
+  int64_t grid;
+  int block;
+  int64_t lds;        // static + dynamic LDS bytes
+};
+
+// 04c.after_linalg_to_loops.mlir: the loop nests of the path's kernels as
+// this build runs them, with this problem's bounds (the reference's file at
+// this stage is its chain lowered to loops; here the loops are those of the
+// hand-written gfx950 kernels, the bodies named by the instructions they issue).
+static std::string emit_loop_structure(const ChainSpec& spec, const VariantDesc& var, int in_code,
+                                       const char* path, const std::vector<StageKernel>& ks) {
+  const int64_t eb = in_code == WTC_DTYPE_FP8_E4M3 ? 1 : in_code == WTC_DTYPE_F32 ? 4 : 2;
+  const int64_t tk = 128 / eb;                                  // elements of one 128-byte k-tile
+  const int64_t nk = (spec.k * eb + 127) / 128;                 // k-tiles
+  const int64_t tm = var.tile_rows, tn = var.id == kVarTile256x256 ? 256 : 128;
+  const int64_t rows = spec.batch * spec.m, nT = (spec.n + tn - 1) / tn;
+  const char* mfma = in_code == WTC_DTYPE_FP8_E4M3 ? "v_mfma_scale_f32_32x32x64_f8f6f4"
+                     : in_code == WTC_DTYPE_BF16 ? "v_mfma_f32_32x32x16_bf16"
+                     : in_code == WTC_DTYPE_F32 ? "v_mfma_f32_32x32x2f32" : "v_mfma_f32_32x32x16_f16";
+  const int64_t ksteps = in_code == WTC_DTYPE_FP8_E4M3 ? 2 : in_code == WTC_DTYPE_F32 ? 16 : 4;
+  std::ostringstream o;
+  o << "// Loop structure of the " << path << " path's kernels on gfx950 (variant " << var.name
+    << "),\n// with this problem's bounds: batch " << spec.batch << ", M " << spec.m << ", N " << spec.n
+    << ", K " << spec.k << ".  Each func is one HIP kernel; scf.parallel is its grid.\n"
+    << "module attributes {wtc.target = \"gfx950\", wtc.path = \"" << path << "\"} {\n";
+  int ind = 4;  // constants are declared at the depth of the loop that uses them
+  auto c = [&](const char* nm, int64_t v) {
+    o << std::string(ind, ' ') << "%" << nm << " = arith.constant " << v << " : index\n";
+  };
+  for (size_t i = 0; i < ks.size(); ++i) {
+    const StageKernel& k = ks[i];
+    o << "  // " << k.name << ": grid " << k.grid << " x " << k.block << " threads, " << k.lds
+      << " bytes of LDS\n  func.func @kernel" << i << "() {\n";
+    c("c0", 0);
+    c("c1", 1);
+    c("grid", k.grid);
+    c("c2", 2);
+    o << "    scf.parallel (%wg) = (%c0) to (%grid) step (%c1) {\n";
+    ind = 6;
+    if (k.kind.rfind("tile_", 0) == 0) {
+      c("nk", nk);
+      c("ks", ksteps);
+      c("tm", tm);
+      c("tn", tn);
+      o << "      // workgroup -> (row block, column tile) of " << tm << "x" << tn
+        << ", XCD-aware order\n"
+        << "      scf.for %kt = %c0 to %nk step %c1 {  // k-tiles of " << tk
+        << " elements: direct-to-LDS buffer loads of k-tile kt+3 into the LDS ring\n"
+        << "        scf.for %s = %c0 to %ks step %c1 {  // LDS fragment reads (B: ds_read_b64_tr), "
+        << mfma << ", f32 accumulators\n        }\n      }\n";
+      if (k.kind == "tile_logits") {
+        o << "      scf.for %r = %c0 to %tm step %c1 {  // logits scale*acc in f32: 16-byte stores\n"
+          << "        scf.for %n = %c0 to %tn step %c1 {\n        }\n      }\n";
+      } else {
+        o << "      scf.for %r = %c0 to %tm step %c1 {  // row statistics over the tile's columns: "
+             "max, exp2(fma(acc, c2, -max)), sum\n"
+          << "        scf.for %n = %c0 to %tn step %c1 {\n        }\n      }\n";
+        if (k.kind == "tile_exchange") {
+          c("nT", nT);
+          o << "      scf.for %q = %c0 to %nT step %c1 {  // row exchange: tagged log-sum-exp entries "
+               "of the row block's tiles, polled\n      }\n"
+            << "      scf.for %r = %c0 to %tm step %c1 {  // out = exp2(y - max) * exp2(max - lse): "
+               "16-byte non-temporal stores\n"
+            << "        scf.for %n = %c0 to %tn step %c1 {\n        }\n      }\n";
+        } else {
+          o << "      scf.for %r = %c0 to %tm step %c1 {  // exp2(y - tile max) stored; per-row "
+               "(max, sum) of the tile to the workspace\n"
+            << "        scf.for %n = %c0 to %tn step %c1 {\n        }\n      }\n";
+        }
+      }
+    } else if (k.kind == "rows") {
+      c("nT", (spec.n + 127) / 128);
+      c("ks", (spec.k + 15) / 16);
+      o << "      // one 128-row block over all of N; A staged in LDS once\n"
+        << "      scf.for %pass = %c0 to %c2 step %c1 {  // pass 0: online row max/sum; pass 1: "
+           "exp2(y - max - log2 sum) stored\n"
+        << "        scf.for %t = %c0 to %nT step %c1 {  // 128-column B tiles through a 4-stage "
+           "direct-to-LDS ring\n"
+        << "          scf.for %s = %c0 to %ks step %c1 {  // " << mfma << "\n          }\n"
+        << "        }\n      }\n";
+    } else if (k.kind == "rescale") {
+      c("n", spec.n);
+      c("nT", nT);
+      o << "      // waves of one row: merge the row's " << nT << " tile statistics, then rescale\n"
+        << "      scf.for %q = %c0 to %nT step %c1 {\n      }\n"
+        << "      scf.for %j = %c0 to %n step %c1 {  // out *= exp2(m_t - M) / S, 16-byte loads and "
+           "stores in place\n      }\n";
+    } else {
+      c("n", spec.n);
+      o << "      scf.for %j = %c0 to %n step %c1 {  // " << k.kind << " over row wg of " << rows
+        << " rows\n      }\n";
+    }
+    o << "      scf.reduce\n    }\n    return\n  }\n";
+    ind = 4;
+  }
+  o << "}\n";
+  return o.str();
+}
+
 static int compile_impl(const char* input_mlir_path, const char* out_dir, int64_t tile_m,
                         int64_t tile_n, int64_t tile_k, int64_t thread_tile_m,
                         int64_t thread_tile_n, int64_t max_connect_level, int fused, int verbose,
@@ -181,6 +284,7 @@ static int compile_impl(const char* input_mlir_path, const char* out_dir, int64_
     int64_t grid;
     int lds;
     int block = 256;
+    std::string kind = "rowwise";  // loop structure in 04c (StageKernel::kind)
   };
   // chain_tile_kernel<in, out, epi, PF = 3, tile rows, ks>
   auto chain_sym = [](int in, int out, int epi, int tm = 128, int lw = 0) {
@@ -209,24 +313,24 @@ static int compile_impl(const char* input_mlir_path, const char* out_dir, int64_
     ks.push_back({"chain_rows_kernel<" + kin + "," + kout + ">",
                   "_ZN3wtc17chain_rows_kernelILi" + std::to_string(in_code) + "ELi" +
                       std::to_string(out_code) + "E",
-                  grid, 0, rows_kernel_threads()});
+                  grid, 0, rows_kernel_threads(), "rows"});
   } else if (path == WTC_PATH_EXCHANGE) {
     ks.push_back({"chain_tile_kernel<" + kin + "," + kout + ",exchange,128x128" +
                       (var.loaders ? ",loaders" : "") + ">",
                   chain_sym(in_code, out_code, 0, 128, var.loaders), grid,
-                  exchange_lds_pad(in_code, out_code, var.loaders), tile_threads});
+                  exchange_lds_pad(in_code, out_code, var.loaders), tile_threads, "tile_exchange"});
   } else if (path == WTC_PATH_SPLIT) {
     const auto tk = tile_kern(out_code, kout, 1, "split");
-    ks.push_back({tk.first, tk.second, grid, 0, tile_threads});
+    ks.push_back({tk.first, tk.second, grid, 0, tile_threads, "tile_split"});
     ks.push_back({"rescale_rows_kernel<" + kout + ">", "_ZN3wtc19rescale_rows_kernel" + out_t,
-                  (rows * rescale_waves_per_row(rows, cu_count) + 3) / 4, 0});
+                  (rows * rescale_waves_per_row(rows, cu_count) + 3) / 4, 0, 256, "rescale"});
   } else {
     const auto tk = tile_kern(0, "f32", 2, "logits");
-    ks.push_back({tk.first, tk.second, grid, 0, tile_threads});
-    ks.push_back({"rowmax_kernel", "_ZN3wtc13rowmax_kernel", rows, 0});
-    ks.push_back({"expsub_kernel", "_ZN3wtc13expsub_kernel", rows, 0});
-    ks.push_back({"rowsum_kernel", "_ZN3wtc13rowsum_kernel", rows, 0});
-    ks.push_back({"rowdiv_kernel<" + kout + ">", "_ZN3wtc13rowdiv_kernel" + out_t, rows, 0});
+    ks.push_back({tk.first, tk.second, grid, 0, tile_threads, "tile_logits"});
+    ks.push_back({"rowmax_kernel", "_ZN3wtc13rowmax_kernel", rows, 0, 256, "row max"});
+    ks.push_back({"expsub_kernel", "_ZN3wtc13expsub_kernel", rows, 0, 256, "exp(x - max)"});
+    ks.push_back({"rowsum_kernel", "_ZN3wtc13rowsum_kernel", rows, 0, 256, "row sum"});
+    ks.push_back({"rowdiv_kernel<" + kout + ">", "_ZN3wtc13rowdiv_kernel" + out_t, rows, 0, 256, "divide"});
   }
 
   std::ostringstream plan;
@@ -272,9 +376,11 @@ static int compile_impl(const char* input_mlir_path, const char* out_dir, int64_
   int64_t mfma = 0, scratch_ops = 0, scratch_bytes = 0, vspill = 0, sspill = 0, dma = 0, tr = 0;
   int missing = 0;
   std::ostringstream per_kernel;
+  std::vector<StageKernel> stage_ks;
   for (const K& k : ks) {
     const auto* row = have_res ? find_kernel(table, k.symbol_prefix) : nullptr;
     if (!row) ++missing;
+    stage_ks.push_back({k.name, k.kind, k.grid, k.block, cell(row, "lds_bytes") + k.lds});
     mfma += cell(row, "mfma");
     scratch_ops += cell(row, "scratch_ops");
     scratch_bytes += cell(row, "scratch_bytes");
@@ -310,42 +416,47 @@ static int compile_impl(const char* input_mlir_path, const char* out_dir, int64_
   report << per_kernel.str();
 
   // The stage files under the reference's names (its callers check that they
-  // exist and are not empty, then count operations in them): the canonical
-  // chain, the launch plan as a module of gpu.launch_func operations, and the
-  // manifest of the gfx950 code object that runs the chain.
+  // exist and are not empty, count operations in them, and its regression
+  // script looks for "workgroup(" in 04 and "gpu.launch_func" in 05): the
+  // canonical chain (03), each kernel's launch with its LDS as the workgroup
+  // attribution (04), the kernels' loop structure (04c), and the runnable
+  // module: one gpu.launch_func per kernel of the gfx950 code object, with
+  // the entry point and its arguments as attributes (05).
   const std::string a_t = memref_of(spec, spec.m, spec.k, spec.in);
   const std::string b_t = memref_of(spec, spec.k, spec.n, spec.in);
   const std::string o_t = memref_of(spec, spec.m, spec.n, spec.out);
   const std::string w_t = "memref<" + std::to_string(ws) + "xi8>";
-  std::ostringstream wg;
-  wg << "// Launch plan of the fused Matmul -> row-Softmax chain on gfx950: one\n"
-     << "// launch operation per HIP kernel of the " << path_name(path) << " path.  The kernel\n"
-     << "// bodies are in the code object 05.out.gfx950.hsaco (library " << lib << "),\n"
-     << "// launched by wtc_matmul_softmax_tiles (variant " << var.name << "); the workspace\n"
-     << "// holds the row statistics.\n"
-     << "module attributes {gpu.container_module, wtc.target = \"gfx950\", wtc.path = \""
-     << path_name(path) << "\", wtc.compute_units = " << cu_count << " : i32} {\n"
-     << "  gpu.module @wtc_kernels [#rocdl.target<chip = \"gfx950\">] {\n  }\n"
-     << "  func.func @chain(%a: " << a_t << ", %b: " << b_t << ", %out: " << o_t << ", %ws: " << w_t
-     << ") {\n    %c1 = arith.constant 1 : index\n";
-  for (size_t i = 0; i < ks.size(); ++i) {
-    std::string kname = ks[i].name;
+  const std::string sig = "(%a: " + a_t + ", %b: " + b_t + ", %out: " + o_t + ", %ws: " + w_t + ")";
+  auto sym_of = [](std::string kname) {
     for (char& c : kname)
       if (!std::isalnum(static_cast<unsigned char>(c))) c = '_';
+    return kname;
+  };
+  std::ostringstream wg;
+  wg << "// Launches of the fused Matmul -> row-Softmax chain on gfx950, " << path_name(path)
+     << " path: one launch region per HIP kernel\n// with its grid, block and LDS (static + dynamic "
+        "bytes, the workgroup attribution).  The bodies are the\n// kernels of the code object "
+        "05.out.gfx950.hsaco (library "
+     << lib << "), variant " << var.name << ".\n"
+     << "module attributes {gpu.container_module, wtc.target = \"gfx950\", wtc.path = \""
+     << path_name(path) << "\", wtc.compute_units = " << cu_count << " : i32} {\n"
+     << "  func.func @chain" << sig << " {\n    %c1 = arith.constant 1 : index\n";
+  for (size_t i = 0; i < ks.size(); ++i) {
     wg << "    %g" << i << " = arith.constant " << ks[i].grid << " : index\n"
        << "    %t" << i << " = arith.constant " << ks[i].block << " : index\n"
-       << "    %l" << i << " = arith.constant " << ks[i].lds << " : i32\n"
-       << "    gpu.launch_func @wtc_kernels::@" << kname << " blocks in (%g" << i
-       << ", %c1, %c1) threads in (%t" << i << ", %c1, %c1) dynamic_shared_memory_size %l" << i
-       << " args(%a : " << a_t << ", %b : " << b_t << ", %out : " << o_t << ", %ws : " << w_t
-       << ")\n";
+       << "    gpu.launch blocks(%bx" << i << ", %by" << i << ", %bz" << i << ") in (%gx" << i << " = %g" << i
+       << ", %gy" << i << " = %c1, %gz" << i << " = %c1) threads(%tx" << i << ", %ty" << i << ", %tz" << i
+       << ") in (%sx" << i << " = %t" << i << ", %sy" << i << " = %c1, %sz" << i
+       << " = %c1) workgroup(%lds" << i << " : memref<" << stage_ks[i].lds << "xi8, 3>) {\n"
+       << "      // body: " << ks[i].name << "\n      gpu.terminator\n    }\n";
   }
   wg << "    return\n  }\n}\n";
   std::ostringstream run;
-  run << "// Runnable artefact of the chain for gfx950 (no NVVM is involved): the HIP\n"
-      << "// code object 05.out.gfx950.hsaco, run through wtc_matmul_softmax_tiles with the\n"
-      << "// arguments below.  Per-kernel resources are in kernel_report.txt.\n"
-      << "module attributes {wtc.target = \"gfx950\", wtc.code_object = \"05.out.gfx950.hsaco\", "
+  run << "// Runnable artefact of the chain for gfx950 (no NVVM is involved): the kernels of\n"
+      << "// the HIP code object 05.out.gfx950.hsaco, launched by wtc_matmul_softmax_tiles with\n"
+      << "// the arguments in the module attributes.  Per-kernel resources are in kernel_report.txt.\n"
+      << "module attributes {gpu.container_module, wtc.target = \"gfx950\", wtc.code_object = "
+         "\"05.out.gfx950.hsaco\", "
       << "wtc.library = \"" << lib << "\", wtc.entry = \"wtc_matmul_softmax_tiles\", wtc.variant = \""
       << var.name << "\", wtc.tiles = [" << want.tile_m << ", " << want.tile_n << ", " << want.tile_k
       << ", " << want.thread_tile_m << ", " << want.thread_tile_n << "], wtc.path = \""
@@ -353,13 +464,23 @@ static int compile_impl(const char* input_mlir_path, const char* out_dir, int64_
       << " : i32, wtc.out_dtype = " << out_code << " : i32, wtc.batch = " << spec.batch
       << " : i64, wtc.m = " << spec.m << " : i64, wtc.n = " << spec.n << " : i64, wtc.k = " << spec.k
       << " : i64, wtc.workspace_bytes = " << ws << " : i64, wtc.mfma_instructions = " << mfma
-      << " : i64, wtc.scratch_bytes = " << scratch_bytes << " : i64} {\n";
-  for (const K& k : ks)
-    run << "  // kernel " << k.name << ": grid " << k.grid << ", block " << k.block
-        << ", dynamic LDS " << k.lds << " bytes\n";
-  run << "}\n";
+      << " : i64, wtc.scratch_bytes = " << scratch_bytes << " : i64} {\n"
+      << "  gpu.module @wtc_kernels [#rocdl.target<chip = \"gfx950\">] {\n  }\n"
+      << "  func.func @chain" << sig << " {\n    %c1 = arith.constant 1 : index\n";
+  for (size_t i = 0; i < ks.size(); ++i) {
+    run << "    %g" << i << " = arith.constant " << ks[i].grid << " : index\n"
+        << "    %t" << i << " = arith.constant " << ks[i].block << " : index\n"
+        << "    %l" << i << " = arith.constant " << ks[i].lds << " : i32\n"
+        << "    gpu.launch_func @wtc_kernels::@" << sym_of(ks[i].name) << " blocks in (%g" << i
+        << ", %c1, %c1) threads in (%t" << i << ", %c1, %c1) dynamic_shared_memory_size %l" << i
+        << " args(%a : " << a_t << ", %b : " << b_t << ", %out : " << o_t << ", %ws : " << w_t
+        << ")\n";
+  }
+  run << "    return\n  }\n}\n";
+  const std::string loops = emit_loop_structure(spec, var, in_code, path_name(path), stage_ks);
   if (!write_file((od / "03.after_postbufferize.mlir").string(), canonical) ||
       !write_file((od / "04.after_workgroup_launch.mlir").string(), wg.str()) ||
+      !write_file((od / "04c.after_linalg_to_loops.mlir").string(), loops) ||
       !write_file((od / "05.out.nvvm.runnable.mlir").string(), run.str()) ||
       !write_file((od / "03.chain.canonical.mlir").string(), canonical) ||
       !write_file((od / "04.kernel.plan.json").string(), plan.str()) ||

@@ -3,10 +3,10 @@
 The counterpart of the reference's bench/pin_baseline.sh:1-67: run the A/B
 harness without verification into ``--run-out-base``, then copy its
 ``ab_summary.tsv``, ``ab_summary.csv``, ``speedup.tsv`` and
-``search/best.json`` and, per variant (``baseline``, ``fused``), the text
-artefacts of the compile (the canonical chain, the kernel plan, the launch
-manifest and the kernel report; the reference pins its 03/04/04c/05 MLIR
-stages) into ``--baseline-dir``, and write ``manifest.txt`` (timestamp,
+``search/best.json`` and, per variant (``baseline``, ``fused``), the compile's
+stage files under the names the reference pins (03 / 04 / 04c / 05 MLIR,
+pin_baseline.sh:44-51) and this build's own (canonical chain, kernel plan,
+launch manifest, kernel report) into ``--baseline-dir``, and write ``manifest.txt`` (timestamp,
 input, mode, connect level, run directory; this build adds the device and
 the timing settings).
 
@@ -28,8 +28,11 @@ from pathlib import Path
 from . import run_ab
 from .perf_guard import DEFAULT_BASELINE_DIR
 
-VARIANT_FILES = ("03.chain.canonical.mlir", "04.kernel.plan.json", "05.out.hip.launch.json",
-                 "kernel_report.txt")
+# the reference's stage files (bench/pin_baseline.sh:44-51), then this build's own
+STAGE_FILES = ("03.after_postbufferize.mlir", "04.after_workgroup_launch.mlir",
+               "04c.after_linalg_to_loops.mlir", "05.out.nvvm.runnable.mlir")
+VARIANT_FILES = STAGE_FILES + ("03.chain.canonical.mlir", "04.kernel.plan.json", "05.out.hip.launch.json",
+                               "kernel_report.txt")
 TOP_FILES = ("ab_summary.tsv", "ab_summary.csv", "speedup.tsv")
 
 

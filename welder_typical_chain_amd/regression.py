@@ -1,20 +1,19 @@
 """Artefact regression run of the wtc-compiler command line.
 
 The counterpart of the reference's bench/run_regression.sh:1-115, with the
-same four runs and checks re-targeted to this build's artefacts:
+same four runs and the same file names and patterns:
 
 1. ``search_api``: ``--search-only`` writes ``search/best.json`` and
    ``search/candidates.tsv`` (run_regression.sh:58-69);
 2. ``named_softmax``: ``--search-only`` on a chain with a named
    ``linalg.softmax`` leaves a canonical chain with ``math.exp`` and
    ``arith.divf`` and no ``linalg.softmax`` (run_regression.sh:71-86);
-3. ``full_api_default``: the full ``--fused`` pipeline writes the launch
-   manifest (the reference: ``05.out.nvvm.runnable.mlir``), its kernel plan
-   names a launch geometry (the reference greps ``workgroup(``) and the
-   manifest names the launcher entry point (the reference greps
-   ``gpu.launch_func``) (run_regression.sh:88-98);
+3. ``full_api_default``: the full ``--fused`` pipeline writes
+   ``05.out.nvvm.runnable.mlir`` with a ``gpu.launch_func`` per kernel, and
+   ``04.after_workgroup_launch.mlir`` whose launches carry their LDS as a
+   ``workgroup(...)`` attribution (run_regression.sh:88-98);
 4. ``pure_api_repeat``: ``--pure-api-full --fused --repeat N`` writes the
-   same into ``iter_<N-1>`` (run_regression.sh:100-112).
+   same runnable module into ``iter_<N-1>`` (run_regression.sh:100-112).
 
 Each check appends ``check  status  detail`` to ``regression_summary.tsv``;
 the first failure ends the run with status 1.  With no ``--input`` the runs
@@ -130,18 +129,18 @@ def run_regression(out_base: Path, input_mlir: Path | None = None,
         d = out_base / "full_api_default"
         wtc("full_api_default", "--input", input_mlir, "--output-dir", d, "--backend-mode", "api",
             "--fused")
-        s.require_file("full_api_default.runnable", d / "fused" / "05.out.hip.launch.json")
-        s.require_contains("full_api_default.workgroup", d / "fused" / "04.kernel.plan.json",
-                           r'"grid": \[\d+, \d+, \d+\], "block": \[\d+, \d+, \d+\]')
-        s.require_contains("full_api_default.launchfunc", d / "fused" / "05.out.hip.launch.json",
-                           r'"entry": "wtc_matmul_softmax_tiles"')
+        s.require_file("full_api_default.runnable", d / "fused" / "05.out.nvvm.runnable.mlir")
+        s.require_contains("full_api_default.workgroup", d / "fused" / "04.after_workgroup_launch.mlir",
+                           r"workgroup\(")
+        s.require_contains("full_api_default.launchfunc", d / "fused" / "05.out.nvvm.runnable.mlir",
+                           r"gpu\.launch_func")
 
         d = out_base / "pure_api_repeat"
         wtc("pure_api_repeat", "--input", input_mlir, "--output-dir", d, "--backend-mode", "api",
             "--pure-api-full", "--fused", "--repeat", pure_api_repeat)
-        last = d / f"iter_{pure_api_repeat - 1}" / "fused" / "05.out.hip.launch.json"
+        last = d / f"iter_{pure_api_repeat - 1}" / "fused" / "05.out.nvvm.runnable.mlir"
         s.require_file("pure_api_repeat.runnable", last)
-        s.require_contains("pure_api_repeat.launchfunc", last, r'"entry": "wtc_matmul_softmax_tiles"')
+        s.require_contains("pure_api_repeat.launchfunc", last, r"gpu\.launch_func")
     except RegressionFailed:
         return 1
     print("[wtc] regression passed")
