@@ -260,6 +260,16 @@ def test_solver_and_compile_per_config(L, tmp_path, name, named):
                                    "score", "estimatedLatency", "profiledMs", "bytesA", "bytesB",
                                    "bytesC", "bytesCut"]
     assert all(len(r.split("\t")) == 13 for r in rows[1:]) and len(rows) >= 2
+    # bytesA: A is streamed once per column tile of the candidate's own width
+    # (256 for the 256x256 tile, 128 otherwise); the rows path reads A once
+    isz = {"f16": 2, "bf16": 2, "fp8": 1, "f32": 4}[cfg.in_dtype]
+    a_bytes = cfg.batch * cfg.m * cfg.k * isz
+    for r in rows[1:]:
+        f = r.split("\t")
+        tile_n, bytes_a = int(f[2]), int(f[9])
+        assert bytes_a in (a_bytes, a_bytes * -(-cfg.n // tile_n)), (f, a_bytes)
+        if tile_n == 256:
+            assert bytes_a == a_bytes * -(-cfg.n // 256), f
     # the reference reads tiles from JSON with a first-match regex (Search.cpp:12-20)
     text = (tmp_path / "best_summary.json").read_text()
     got = [int(re.search(rf'"{k}"\s*:\s*(-?[0-9]+)', text).group(1))

@@ -119,6 +119,67 @@ def test_profiler_f16_conversion_differs_only_on_ties():
     assert lib.wtc_ref_f32_to_f16(y) == lib.wtc_ref_f32_to_f16_profiler(y)
 
 
+def _f16_ulp(a: np.ndarray) -> np.ndarray:
+    """f16 spacing at |a| (float64): 2^(e - 10) in the binade 2^e, 2^-24 below 2^-14."""
+    e = np.floor(np.log2(np.maximum(np.abs(a), 2.0 ** -40)))
+    return 2.0 ** (np.maximum(e, -14.0) - 10.0)
+
+
+def _profiler_closed_form(x: np.ndarray) -> np.ndarray:
+    """Round to the nearest f16, ties away from zero, overflow to inf (the
+    rounding WelderProfilerEval.h:50-100 implements), restated in float64."""
+    a = np.abs(x.astype(np.float64))
+    ulp = _f16_ulp(a)
+    r = np.floor(a / ulp + 0.5) * ulp
+    r = np.where(r > 65504.0, np.inf, r)
+    return (np.copysign(r, x.astype(np.float64))).astype(np.float16).view(np.uint16)
+
+
+def test_profiler_f16_conversion_pinned():
+    """The profiler's f32 -> f16 over every range: on values that are not
+    exact ties it equals IEEE round-to-nearest (numpy), on exact ties it
+    rounds away from zero, including ties whose rounding carries into the
+    exponent and ties at the subnormal and overflow ends."""
+    lib = O.lib()
+    conv = np.vectorize(lambda v: lib.wtc_ref_f32_to_f16_profiler(np.float32(v)), otypes=[np.uint16])
+    rng = np.random.default_rng(11)
+    parts = [
+        rng.uniform(2.0 ** -14, 65504.0, 4000),          # normal
+        2.0 ** rng.uniform(-14, 16, 4000),                # normal, every binade
+        rng.uniform(2.0 ** -25, 2.0 ** -14, 3000),        # subnormal results
+        rng.uniform(0.0, 2.0 ** -25, 500),                # below half the smallest subnormal
+        rng.uniform(65504.0, 2.0 ** 17, 1000),            # overflow side
+    ]
+    x = np.concatenate(parts).astype(np.float32)
+    x = np.concatenate([x, -x])
+    q = np.abs(x.astype(np.float64)) / _f16_ulp(x.astype(np.float64))
+    tie = (q - np.floor(q)) == 0.5
+    got = conv(x)
+    np.testing.assert_array_equal(got[~tie], x[~tie].astype(np.float16).view(np.uint16))
+    np.testing.assert_array_equal(got[tie], _profiler_closed_form(x[tie]))
+    # exact ties: (k + 1/2) ulp in normal binades, at the binade top (k = 2047:
+    # the rounding carries into the exponent), in the subnormal range, the
+    # smallest subnormal's tie 2^-25, and the overflow tie 65520
+    e = rng.integers(-14, 16, 3000)
+    k = rng.integers(1024, 2048, 3000)
+    ties = [(k + 0.5) * 2.0 ** (e - 10.0), (2047 + 0.5) * 2.0 ** (np.arange(-14, 16) - 10.0),
+            (rng.integers(1, 1024, 1000) + 0.5) * 2.0 ** -24, np.array([2.0 ** -25, 65520.0])]
+    t = np.concatenate(ties).astype(np.float32)
+    t = np.concatenate([t, -t])
+    assert ((np.abs(t.astype(np.float64)) / _f16_ulp(t.astype(np.float64))) % 1 == 0.5).all()
+    got = conv(t)
+    np.testing.assert_array_equal(got, _profiler_closed_form(t))
+    # against IEEE these ties differ exactly where RNE rounds down to even
+    rne = t.astype(np.float16).view(np.uint16)
+    assert (got != rne).any() and (got == rne).any()
+    assert lib.wtc_ref_f32_to_f16_profiler(np.float32(2047.5 * 2.0 ** -10)) == 0x4000  # carry to 2.0
+    assert lib.wtc_ref_f32_to_f16_profiler(np.float32(65520.0)) == 0x7C00
+    assert lib.wtc_ref_f32_to_f16_profiler(np.float32(2.0 ** -25)) == 0x0001
+    for v in (np.inf, -np.inf):
+        assert lib.wtc_ref_f32_to_f16_profiler(np.float32(v)) == np.float16(v).view(np.uint16)
+    assert lib.wtc_ref_f32_to_f16_profiler(np.float32(np.nan)) & 0x7C00 == 0x7C00
+
+
 def test_bf16_against_torch():
     torch = pytest.importorskip("torch")
     rng = np.random.default_rng(1)

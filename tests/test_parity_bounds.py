@@ -55,7 +55,7 @@ def test_bound_covers_f32_accumulation(kind, toward_zero):
     rows = np.arange(4)
     scale = 0.37
     logits, _ = O.chain_rows(a.astype(np.float32), b.astype(np.float32), rows, scale)
-    bound = logit_error_bound(a, b, rows, scale, logits, kind)
+    bound = logit_error_bound(a, b, rows, scale, logits, kind, worst_case=True)
     worst = 0.0
     for r in rows:
         got = scale * _f32_accumulate(a[r], b, toward_zero, round_products=kind == "f32")
@@ -78,9 +78,51 @@ def test_bound_scales_with_the_accumulation():
     rows = np.arange(2)
     l1, _ = O.chain_rows(a.astype(np.float32), b.astype(np.float32), rows, 1.0)
     l2, _ = O.chain_rows(a.astype(np.float32), b.astype(np.float32), rows, 2.0)
-    e1 = logit_error_bound(a, b, rows, 1.0, l1, "f16") - 4 * U32 * np.abs(l1)
-    e2 = logit_error_bound(a, b, rows, 2.0, l2, "f16") - 4 * U32 * np.abs(l2)
+    e1 = logit_error_bound(a, b, rows, 1.0, l1, "f16", worst_case=True) - 4 * U32 * np.abs(l1)
+    e2 = logit_error_bound(a, b, rows, 2.0, l2, "f16", worst_case=True) - 4 * U32 * np.abs(l2)
     np.testing.assert_allclose(e2, 2 * e1, rtol=1e-12)
     z = np.zeros_like(a)
     lz, _ = O.chain_rows(z.astype(np.float32), b.astype(np.float32), rows, 1.0)
     assert (logit_error_bound(z, b, rows, 1.0, lz, "f16") == 0).all()
+
+
+@pytest.mark.parametrize("kind", ["f16", "fp8", "f32"])
+def test_gate_covers_round_to_nearest_accumulation(kind):
+    """The gate (the smaller of the worst case and LAMBDA u sqrt(sum s_i^2))
+    covers f32 round-to-nearest accumulation in k order with room to spare."""
+    k, n = 2048, 64
+    a, b = _inputs(kind, k, n, seed=5)
+    rows = np.arange(4)
+    logits, _ = O.chain_rows(a.astype(np.float32), b.astype(np.float32), rows, 1.0)
+    gate = logit_error_bound(a, b, rows, 1.0, logits, kind)
+    assert (gate <= logit_error_bound(a, b, rows, 1.0, logits, kind, worst_case=True)).all()
+    for r in rows:
+        got = _f32_accumulate(a[r], b, False, round_products=kind == "f32")
+        err = np.abs(got - logits[r])
+        assert (err <= 0.5 * gate[r]).all(), (kind, float((err / gate[r]).max()))
+
+
+def test_gate_on_c5_is_tight_and_catches_a_scale_error():
+    """On C5's inputs (fp8, K = 4096) the worst-case allowance would let 15-19 %
+    through on the largest outputs; the gate allows about 1 %, stays below the
+    ceiling, and rejects outputs computed with a logit scale 2 % off (a
+    mistake planted in the oracle's softmax here, on the CPU)."""
+    from welder_typical_chain_amd.configs import CONFIGS
+    from .parity_util import LOGIT_REL_CEILING, compare_rows
+    cfg = CONFIGS["C5"]
+    inp = O.make_inputs(cfg, seed=0, m=64)
+    rows = np.array([0, 37])
+    logits, probs = O.chain_rows(inp.a[0], inp.b[0], rows, inp.scale)
+    worst = logit_error_bound(inp.a[0], inp.b[0], rows, inp.scale, logits, "fp8", worst_case=True)
+    gate = logit_error_bound(inp.a[0], inp.b[0], rows, inp.scale, logits, "fp8")
+    rel_worst = float(np.expm1(worst + worst.max(axis=1, keepdims=True)).max())
+    rel_gate = float(np.expm1(gate + gate.max(axis=1, keepdims=True)).max())
+    assert rel_worst > 0.1 > LOGIT_REL_CEILING > 0.02 > rel_gate, (rel_worst, rel_gate)
+    # the oracle's own outputs pass
+    compare_rows(probs, probs, logits, "f16", "c5-exact", "fp8", gate)
+    # a 2 % scale error does not
+    y = logits * 1.02
+    bad = np.exp(y - y.max(axis=1, keepdims=True))
+    bad /= bad.sum(axis=1, keepdims=True)
+    with pytest.raises(AssertionError):
+        compare_rows(bad, probs, logits, "f16", "c5-scale", "fp8", gate)

@@ -103,7 +103,7 @@ std::vector<Candidate> solve(const ChainSpec& s, int64_t /*max_connect_level*/,
     if (cs.empty()) continue;
     const Choice& c = cs.front();
     const int64_t nrb = (s.m + v.tile_rows - 1) / v.tile_rows;
-    const int64_t nt = (s.n + 127) / 128;
+    const int64_t nt = (s.n + v.tile_n - 1) / v.tile_n;  // the variant's column tiles
     Candidate cand;
     cand.tiles = TileParams{v.tile_m, v.tile_n, v.tile_k, v.thread_tile_m, v.thread_tile_n};
     cand.variant = v.name;

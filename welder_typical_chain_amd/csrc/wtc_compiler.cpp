@@ -107,15 +107,15 @@ bool canonicalize(const std::string& input, const fs::path& out_mlir, wtc::Chain
     return false;
   }
   if (!contains(canonical, "linalg.matmul") && !contains(canonical, "linalg.batch_matmul")) {
-    diag = "canonicalized IR lost linalg.matmul unexpectedly";
+    diag = "canonicalize: the chain's matmul is missing from " + out_mlir.string();
     return false;
   }
   if (contains(canonical, "linalg.softmax")) {
-    diag = "softmax decomposition did not run: linalg.softmax remains";
+    diag = "canonicalize: a named linalg.softmax is still present in " + out_mlir.string() + " (it must be decomposed)";
     return false;
   }
   if (!contains(canonical, "math.exp") || !contains(canonical, "arith.divf")) {
-    diag = "canonicalized IR does not contain expected softmax decomposition ops";
+    diag = "canonicalize: " + out_mlir.string() + " lacks the exponential (math.exp) or the division (arith.divf) of a decomposed softmax";
     return false;
   }
   return true;
@@ -126,22 +126,22 @@ bool tag(const fs::path& canonical_path, const wtc::ChainSpec& spec, const fs::p
          const fs::path& tags_json_path, std::string& diag) {
   std::string text;
   if (!wtc::read_file(canonical_path.string(), text) || text.empty()) {
-    diag = "failed to read input MLIR for tagging: " + canonical_path.string();
+    diag = "tag: cannot read " + canonical_path.string() + " (missing or empty)";
     return false;
   }
   if ((count_of(text, "linalg.matmul") + count_of(text, "linalg.batch_matmul")) == 0 ||
       count_of(text, "linalg.generic") == 0) {
-    diag = "tagging expects matmul + generic softmax decomposition in input";
+    diag = "tag: " + canonical_path.string() + " needs a matmul followed by linalg.generic softmax stages";
     return false;
   }
   std::string tagged, tags_json;
   wtc::tag_chain(text, spec, canonical_path.string(), tagged, tags_json);
   if (!wtc::write_file(tagged_path.string(), tagged)) {
-    diag = "failed to write tagged MLIR: " + tagged_path.string();
+    diag = "tag: cannot write " + tagged_path.string();
     return false;
   }
   if (!wtc::write_file(tags_json_path.string(), tags_json)) {
-    diag = "failed to write tags json: " + tags_json_path.string();
+    diag = "tag: cannot write " + tags_json_path.string();
     return false;
   }
   return true;
@@ -499,7 +499,7 @@ int main(int argc, char** argv) {
     Options it = o;
     it.output_dir = (fs::path(o.output_dir) / ("iter_" + std::to_string(i))).string();
     if (o.verbose)
-      std::cout << "[wtc] repeat " << (i + 1) << "/" << repeat << ", output-dir=" << it.output_dir
+      std::cout << "[wtc] pipeline run " << (i + 1) << " of " << repeat << " into " << it.output_dir
                 << "\n";
     const int rc = run_pipeline(it);
     if (rc != 0) {
