@@ -10,9 +10,10 @@
  * A HIP code object has no such text form, so the launch is a C call taking
  * device pointers.  All buffers are owned by the caller; the library owns
  * only the default workspaces (one per stream that passed a NULL
- * `workspace`; they grow when a larger problem needs it and are never freed
- * before the process ends, since a captured graph may hold their address) and
- * one pinned host word per device (the timeout mailbox).
+ * `workspace`; they grow when a larger problem needs it, keeping the smaller
+ * buffer too, since a captured graph may hold its address, and are freed by
+ * wtc_release_stream or at process end) and one small pinned host array per
+ * device (the timeout mailbox: one word per stream).
  *
  * Layouts are dense row-major: A [batch][m][k], B [batch][k][n],
  * out [batch][m][n] (the reference's strides [K,1] / [N,1] / [N,1],
@@ -33,8 +34,12 @@
  * not for streams being captured into a graph).  If other work -- another
  * process, or a replayed graph -- holds the CUs its tiles wait for, the wait
  * ends after a bounded time and the call's output is wrong: that is reported
- * as WTC_ERR_TIMEOUT by the next wtc_matmul_softmax or wtc_check_status on
- * the device (see also wtc_read_error_flags).
+ * as WTC_ERR_TIMEOUT to the same stream, by its next call of any entry point
+ * made after the kernel finished (which then does nothing else) or by
+ * wtc_check_status of that stream; calls on other streams are not affected
+ * (see also wtc_read_error_flags).  A graph's call reports to the stream it
+ * was captured on.  The wait limit defaults to 200 times the cost model's
+ * estimate of the call, between 5 ms and 2 s (wtc_set_exchange_wait_limit).
  */
 #ifndef WTC_HIP_H
 #define WTC_HIP_H
@@ -52,7 +57,7 @@ extern "C" {
 #define WTC_ERR_WORKSPACE 2    /* caller workspace too small */
 #define WTC_ERR_HIP 3          /* a HIP runtime call failed */
 #define WTC_ERR_UNSUPPORTED 4  /* shape / path combination not available */
-#define WTC_ERR_TIMEOUT 5      /* an earlier exchange-path call on this device timed out
+#define WTC_ERR_TIMEOUT 5      /* an earlier exchange-path call on this stream timed out
                                   waiting for its tiles; its output is wrong (reported
                                   once; the call that reports it does nothing else) */
 
@@ -138,13 +143,16 @@ int wtc_profile_tiles(int64_t batch, int64_t m, int64_t n, int64_t k, int in_dty
  * hipMalloc).  Same arguments, paths and results as wtc_matmul_softmax,
  * except that the workspace is a fixed array of WTC_NOALLOC_SCRATCH_BYTES
  * that the library holds on each GPU until the process ends (its address is
- * looked up once per device, on the first call there).  It calls no
- * hipMalloc, hipFree or other allocating routine, so it also creates no
- * timeout mailbox or exchange event itself: a timed-out exchange wait is
- * reported by the next call (or wtc_check_status) only once an allocating
- * entry point has run on the device, and exchange calls on different
- * streams are ordered only in that case too; the array's own diagnostic
- * words are always read by wtc_read_error_flags(NULL, ...).  Problems whose
+ * looked up once per device).  It calls no hipMalloc, hipFree or other
+ * allocating routine, so it also creates no timeout mailbox or exchange
+ * event itself.  Set-up: call wtc_check_status once on the device, outside
+ * graph capture, before the first call of this entry point there: that call
+ * makes the device's set-up (kernel attributes, the array's address, the
+ * mailbox, the exchange event), after which calls of this entry point do
+ * none and may be captured.  Without it the first call on a device does the
+ * set-up other than the mailbox and event (it must then not be captured),
+ * and a timed-out exchange wait is reported only through the array's
+ * diagnostic words (wtc_read_error_flags(NULL, ...)).  Problems whose
  * workspace (wtc_matmul_softmax_workspace_size) exceeds the array get
  * WTC_ERR_WORKSPACE.  Every call on a GPU shares that GPU's array: calls
  * that overlap on one GPU (other streams, other host threads) race and must
@@ -191,14 +199,24 @@ int wtc_plan_tiles(int64_t batch, int64_t m, int64_t n, int64_t k, int in_dtype,
 int wtc_read_error_flags(void *workspace, uint32_t *flags, int clear);
 
 /* Synchronises `stream` (a hipStream_t, NULL = the null stream) and returns
- * WTC_ERR_TIMEOUT if an exchange-path wait of any call on the current device
- * timed out since the last report, else WTC_OK. */
+ * WTC_ERR_TIMEOUT if an exchange-path wait of a call on that stream timed out
+ * since the last report, else WTC_OK.  Also makes the current device's
+ * set-up (see wtc_matmul_softmax_noalloc). */
 int wtc_check_status(void *stream);
 
 /* Limit of every exchange-path wait, in ticks of the 100 MHz real-time clock
- * (0 = the default, 2 s).  Applies to calls made after it; for tests of the
- * timeout reporting. */
+ * (0 = automatic: 200 times the cost model's estimate of the call, at least
+ * 5 ms, at most 2 s).  Applies to calls made after it. */
 int wtc_set_exchange_wait_limit(uint64_t ticks);
+
+/* Synchronises `stream`, frees its default workspace (and the smaller ones it
+ * replaced) and gives back its timeout-mailbox word; call it before
+ * destroying a stream that made NULL-workspace calls.  Graphs captured on the
+ * stream with its default workspace must not be replayed afterwards.  Returns
+ * WTC_ERR_TIMEOUT if a timeout of the stream was still unreported (the
+ * resources are freed all the same).  No counterpart in the reference, whose
+ * launches take caller buffers only. */
+int wtc_release_stream(void *stream);
 
 /* Message of the last failing call on this thread ("" if none). */
 const char *wtc_last_error(void);

@@ -4,7 +4,8 @@
   few ticks from the host, so the first tiles of every row block give up
   (every kernel still exits normally: all waits are bounded), and the error
   must come back as WTC_ERR_TIMEOUT from wtc_check_status and from the next
-  call, once.
+  call on the same stream, once; a call on another stream is not affected.
+* wtc_release_stream frees a stream's default workspace.
 * Default workspaces: one per stream, grow-only; none is allocated while the
   stream is being captured; a graph captured with the default workspace still
   replays correctly after an eager call of a larger shape grew it.
@@ -86,6 +87,94 @@ def test_exchange_timeout_is_reported(native_lib):
     flags, longest, timeouts = read_diagnostics(ws)
     print(f"[gpu-case] clean call: max abs err {err:.2e}, longest wait {longest / 100:.1f} us")
     assert err < 2e-3 and flags == 0 and timeouts == 0
+
+
+@needs_gpu
+def test_timeout_is_reported_to_its_own_stream(native_lib):
+    """Stream A's call times out (wait limit of 2 ticks); stream B's next call
+    runs and is correct; A's next call reports WTC_ERR_TIMEOUT and does
+    nothing else; the call after that on A runs and is correct."""
+    from welder_typical_chain_amd import _lib
+    from welder_typical_chain_amd.chain import (check_status, matmul_softmax, new_workspace,
+                                                read_diagnostics, release_stream,
+                                                set_exchange_wait_limit, workspace_size)
+    _announce("two streams: A times out at a 2-tick limit, B runs, A's next call reports")
+    m = n = 2048
+    k = 256
+    a, b = _inputs(m, n, k, 5)
+    ref = torch.softmax(a.float() @ b.float(), dim=-1)
+    nbytes = workspace_size(1, m, n, k, 1, 1, "exchange")
+    ws_a, ws_b = new_workspace(nbytes), new_workspace(nbytes)
+    s_a, s_b = torch.cuda.Stream(), torch.cuda.Stream()
+    for s in (s_a, s_b):
+        s.wait_stream(torch.cuda.current_stream())
+    try:
+        set_exchange_wait_limit(2)
+        timed_out = False
+        with torch.cuda.stream(s_a):
+            # whether a call times out at this limit depends on the order its tiles start in
+            for _ in range(8):
+                matmul_softmax(a, b, path="exchange", workspace=ws_a)
+                s_a.synchronize()
+                if read_diagnostics(ws_a)[2] > 0:
+                    timed_out = True
+                    break
+        assert timed_out
+    finally:
+        set_exchange_wait_limit(0)
+    with torch.cuda.stream(s_b):
+        out_b = matmul_softmax(a, b, path="exchange", workspace=ws_b)
+        check_status()  # stream B has nothing to report
+    s_b.synchronize()
+    err_b = float((out_b.float() - ref).abs().max())
+    flags_b = read_diagnostics(ws_b)
+    print(f"[gpu-case] stream B: max abs err {err_b:.2e}, diagnostics {flags_b}", flush=True)
+    assert err_b < 2e-3 and flags_b[0] == 0 and flags_b[2] == 0
+    with torch.cuda.stream(s_a):
+        stale = torch.full((m, n), 7.0, dtype=torch.float16, device="cuda")
+        with pytest.raises(_lib.WtcError) as ei:
+            matmul_softmax(a, b, out=stale, path="exchange", workspace=ws_a)
+        assert ei.value.code == _lib.WTC_ERR_TIMEOUT
+        assert "stream" in str(ei.value)
+        check_status()  # reported once
+        out_a = matmul_softmax(a, b, path="exchange", workspace=ws_a, check=True)
+    s_a.synchronize()
+    assert bool((stale == 7.0).all()), "the reporting call wrote its output"
+    err_a = float((out_a.float() - ref).abs().max())
+    flags_a = read_diagnostics(ws_a)
+    print(f"[gpu-case] stream A after the report: max abs err {err_a:.2e}, diagnostics {flags_a}")
+    assert err_a < 2e-3 and flags_a[0] == 0 and flags_a[2] == 0
+    release_stream(s_a)
+    release_stream(s_b)
+
+
+@needs_gpu
+def test_release_stream_frees_its_default_workspace(native_lib):
+    from welder_typical_chain_amd.chain import matmul_softmax, release_stream, workspace_size
+    m, n, k = 2048, 16384, 64
+    need = workspace_size(1, m, n, k, 1, 1, "unfused")
+    _announce(f"default workspace of {need >> 20} MiB on a new stream, then released")
+    a, b = _inputs(m, n, k, 6)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info()[0]
+    with torch.cuda.stream(s):
+        out = matmul_softmax(a, b, path="unfused")
+    s.synchronize()
+    free1 = torch.cuda.mem_get_info()[0]
+    release_stream(s)
+    free2 = torch.cuda.mem_get_info()[0]
+    print(f"[gpu-case] free MiB: {free0 >> 20} -> {free1 >> 20} -> {free2 >> 20}", flush=True)
+    out_bytes = out.numel() * out.element_size()
+    assert free0 - free1 >= need - out_bytes // 2  # the workspace (and perhaps the output)
+    assert free2 - free1 >= need * 9 // 10
+    # the stream works again afterwards, with a new default workspace
+    with torch.cuda.stream(s):
+        again = matmul_softmax(a, b, path="unfused")
+    s.synchronize()
+    assert torch.equal(again, out)
+    release_stream(s)
 
 
 @needs_gpu

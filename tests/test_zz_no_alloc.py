@@ -3,7 +3,8 @@ the C-ABI, against wtc_matmul_softmax with a caller workspace: the same
 kernels run, so the outputs must be identical bit for bit, on two calls in a
 row (the second smaller, reusing the scratch array), on every path; a
 problem whose workspace exceeds the array is refused; a captured call
-replays correctly.
+replays correctly, also when it is the first call of the entry point in a
+process (after the documented set-up call, wtc_check_status).
 """
 from __future__ import annotations
 
@@ -66,12 +67,10 @@ def test_noalloc_matches_workspace_entry_point(native_lib, path):
         exp = torch.softmax(a.float() @ b.float(), dim=-1)
         d = (out.float() - exp).abs()
         assert bool((d <= 2e-3 + 1e-2 * exp).all())
-    flags = (torch.zeros(3, dtype=torch.int32))
     import ctypes
     words = (ctypes.c_uint32 * 3)()
     assert lib.wtc_read_error_flags(None, words, 1) == 0
     assert words[0] == 0 and words[2] == 0, list(words)
-    del flags
 
 
 @needs_gpu
@@ -117,3 +116,67 @@ def test_noalloc_in_a_captured_graph(native_lib):
         torch.cuda.synchronize()
         assert torch.equal(out, ref), f"replay {rep}"
         del junk
+
+
+_FIRST_CALL_CAPTURED = r"""
+import ctypes, sys
+import torch
+from welder_typical_chain_amd import _lib
+lib = _lib.lib()
+m, n, k = 1024, 2048, 256
+g = torch.Generator(device="cuda")
+g.manual_seed(21)
+a = (torch.randn((m, k), generator=g, device="cuda") / 16.0).half()
+b = torch.randn((k, n), generator=g, device="cuda").half()
+out = torch.zeros((m, n), dtype=torch.float16, device="cuda")
+ref = torch.zeros_like(out)
+s = torch.cuda.Stream()
+s.wait_stream(torch.cuda.current_stream())
+torch.cuda.synchronize()
+def call(o):
+    return lib.wtc_matmul_softmax_noalloc(a.data_ptr(), b.data_ptr(), o.data_ptr(), 1, m, n, k,
+                                          _lib.DTYPE_F16, _lib.DTYPE_F16, 1.0, 1.0, 1.0,
+                                          _lib.PATH_EXCHANGE, s.cuda_stream)
+# the library's first call in this process: the device's set-up
+assert lib.wtc_check_status(s.cuda_stream) == 0, lib.wtc_last_error()
+print("[child] set-up done; capturing the first noalloc call", flush=True)
+graph = torch.cuda.CUDAGraph()
+with torch.cuda.graph(graph, stream=s):
+    rc = call(out)
+assert rc == 0, lib.wtc_last_error()
+torch.cuda.synchronize()
+with torch.cuda.stream(s):
+    assert call(ref) == 0, lib.wtc_last_error()
+torch.cuda.synchronize()
+exp = torch.softmax(a.float() @ b.float(), dim=-1)
+assert float((ref.float() - exp).abs().max()) < 2e-3
+for rep in range(3):
+    out.zero_()
+    junk = (a.float() * 3.0).sum()
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref), f"replay {rep}"
+    del junk
+words = (ctypes.c_uint32 * 3)()
+assert lib.wtc_read_error_flags(None, words, 1) == 0
+assert words[0] == 0 and words[2] == 0, list(words)
+assert lib.wtc_check_status(s.cuda_stream) == 0, lib.wtc_last_error()
+print("[child] OK", flush=True)
+"""
+
+
+@needs_gpu
+def test_noalloc_first_call_captured_after_set_up(native_lib):
+    """In a fresh process, wtc_check_status makes the device's set-up and the
+    first noalloc call is made under graph capture: its replays match an
+    eager noalloc call bit for bit."""
+    import os
+    import subprocess
+    import sys
+    _announce("fresh process: wtc_check_status, then the first noalloc call captured")
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, "-c", _FIRST_CALL_CAPTURED], cwd=root, capture_output=True,
+                       text=True, timeout=240)
+    print(r.stdout[-2000:], r.stderr[-2000:], flush=True)
+    assert r.returncode == 0 and "[child] OK" in r.stdout

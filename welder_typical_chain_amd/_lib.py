@@ -79,6 +79,7 @@ SIGNATURES = {
     "wtc_read_error_flags": (ctypes.c_int, [_c_p, ctypes.POINTER(ctypes.c_uint32), ctypes.c_int]),
     "wtc_check_status": (ctypes.c_int, [_c_p]),
     "wtc_set_exchange_wait_limit": (ctypes.c_int, [ctypes.c_uint64]),
+    "wtc_release_stream": (ctypes.c_int, [_c_p]),
     "wtc_last_error": (ctypes.c_char_p, []),
     "wtc_version": (ctypes.c_char_p, []),
     "welder_compile_typical_chain_to_nvvm": (ctypes.c_int, [

@@ -116,7 +116,7 @@ def matmul_softmax(a: torch.Tensor, b: torch.Tensor, *, out: torch.Tensor | None
 
 def check_status(device: torch.device | str | None = None) -> None:
     """Synchronise the current stream of `device` and raise WtcError if an
-    exchange-path wait of any call on the device timed out since the last
+    exchange-path wait of a call on that stream timed out since the last
     report (wtc_check_status)."""
     dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
     with torch.cuda.device(dev):
@@ -125,8 +125,18 @@ def check_status(device: torch.device | str | None = None) -> None:
 
 
 def set_exchange_wait_limit(ticks: int) -> None:
-    """Limit of each exchange-path wait in 100 MHz ticks (0 = default, 2 s)."""
+    """Limit of each exchange-path wait in 100 MHz ticks (0 = automatic:
+    200 times the cost model's estimate of the call, between 5 ms and 2 s)."""
     _lib.check(_lib.lib().wtc_set_exchange_wait_limit(int(ticks)))
+
+
+def release_stream(stream: torch.cuda.Stream | None = None) -> None:
+    """Free the default workspace and the timeout-mailbox word of `stream`
+    (default: the current stream) after synchronising it
+    (wtc_release_stream); raises WtcError for a timeout it still held."""
+    s = stream if stream is not None else torch.cuda.current_stream()
+    with torch.cuda.device(s.device):
+        _lib.check(_lib.lib().wtc_release_stream(s.cuda_stream))
 
 
 def read_error_flags(workspace: torch.Tensor | None = None, clear: bool = True) -> int:

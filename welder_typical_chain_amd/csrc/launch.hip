@@ -56,12 +56,28 @@ using namespace wtc;
 
 constexpr int kTile = 128;            // BN of chain_tile_kernel, rows of the exchange tiles
 constexpr int kRescaleRowsPerWg = 4;  // rescale_rows_kernel
-constexpr uint64_t kDefaultSpinTicks = 200000000ull;  // 2 s of the 100 MHz clock
 constexpr int kMaxDevices = 64;
+// Timeout mailbox words per device: slot 0 is shared by the streams that
+// found every other slot taken, slots 1.. belong to one stream each.
+constexpr int kMailboxSlots = 64;
 constexpr int64_t kMinDefaultWorkspace = 1 << 20;
 
 thread_local std::string g_last_error;
-std::atomic<uint64_t> g_spin_ticks{kDefaultSpinTicks};
+std::atomic<uint64_t> g_spin_ticks{0};  // 0: derived from the plan's estimate
+
+// Limit of one exchange-path wait, in 100 MHz ticks: the caller's setting,
+// else 200 times the cost model's estimate of the whole call, at least 5 ms
+// (a wait of tiles that are all resident ends within the kernel's duration;
+// the floor leaves room for launch skew and time-slicing with other
+// processes) and at most 2 s.
+uint64_t wait_limit_ticks(double est_us) {
+  const uint64_t set = g_spin_ticks.load();
+  if (set) return set;
+  double us = 200.0 * est_us;
+  if (!(us >= 5000.0)) us = 5000.0;
+  if (us > 2.0e6) us = 2.0e6;
+  return (uint64_t)(us * 100.0);
+}
 
 int fail(int code, const std::string& msg) {
   g_last_error = msg;
@@ -248,17 +264,24 @@ struct StreamWorkspace {
   void* ptr;
   size_t bytes;
 };
+struct RetiredBuffer {
+  hipStream_t stream;
+  void* ptr;
+};
 
 struct DeviceState {
   bool init = false;
   int cu_count = 0;
   int occ[4][3] = {};  // exchange-kernel workgroups per CU (fewest of the layouts), [in_dt][out_dt]
   std::vector<StreamWorkspace> ws;
-  std::vector<void*> retired;
-  // Host-visible word the exchange kernels set when a wait times out
-  // (pinned, mapped host memory): the next call on the device reports it.
+  std::vector<RetiredBuffer> retired;
+  // Host-visible words the exchange kernels set when a wait times out
+  // (pinned, mapped host memory, kMailboxSlots words), one per stream: the
+  // next call on the stream of the timed-out call reports it.
   volatile uint32_t* mailbox_host = nullptr;
   uint32_t* mailbox_dev = nullptr;
+  hipStream_t slot_stream[kMailboxSlots] = {};
+  bool slot_used[kMailboxSlots] = {};
   // Cross-stream ordering of exchange-path calls: an event recorded after
   // every exchange launch, and the stream it was recorded on.
   hipEvent_t exch_event = nullptr;
@@ -306,8 +329,9 @@ int device_state(int dev, DeviceState** out, bool host_objects = true) {
   }
   if (host_objects && !s.mailbox_host) {
     void* mb = nullptr;
-    HIP_TRY(hipHostMalloc(&mb, 64, hipHostMallocMapped | hipHostMallocCoherent));
-    std::memset(mb, 0, 64);
+    HIP_TRY(hipHostMalloc(&mb, kMailboxSlots * sizeof(uint32_t),
+                          hipHostMallocMapped | hipHostMallocCoherent));
+    std::memset(mb, 0, kMailboxSlots * sizeof(uint32_t));
     void* mbd = nullptr;
     HIP_TRY(hipHostGetDevicePointer(&mbd, mb, 0));
     s.mailbox_host = static_cast<volatile uint32_t*>(mb);
@@ -362,7 +386,7 @@ int default_workspace(DeviceState* s, int64_t need, void** ws, hipStream_t strea
     return rc;
   }
   if (cur) {
-    s->retired.push_back(cur->ptr);
+    s->retired.push_back(RetiredBuffer{stream, cur->ptr});
     cur->ptr = p;
     cur->bytes = (size_t)bytes;
   } else {
@@ -417,13 +441,76 @@ int launch_tile(const void* kern, int threads, int64_t grid, int lds_dyn,
   return WTC_OK;
 }
 
-// A timed-out exchange wait of an earlier call on this device, reported once.
-int take_mailbox(DeviceState* ds) {  // no mailbox yet: nothing to report
-  if (ds->mailbox_host && *ds->mailbox_host != 0u &&
-      __atomic_exchange_n(const_cast<uint32_t*>(ds->mailbox_host), 0u, __ATOMIC_SEQ_CST) != 0u) {
+// The mailbox slot of `stream`: its own, given out on its first call, or
+// slot 0, shared by the streams that came when all others were taken.  The
+// table is a fixed array: looking a stream up allocates nothing.
+int mailbox_slot(DeviceState* ds, hipStream_t stream) {
+  for (int i = 1; i < kMailboxSlots; ++i)
+    if (ds->slot_used[i] && ds->slot_stream[i] == stream) return i;
+  for (int i = 1; i < kMailboxSlots; ++i)
+    if (!ds->slot_used[i]) {
+      ds->slot_used[i] = true;
+      ds->slot_stream[i] = stream;
+      if (ds->mailbox_host) ds->mailbox_host[i] = 0u;
+      return i;
+    }
+  return 0;
+}
+
+// The device address of `stream`'s mailbox word (NULL while the device has
+// no mailbox: the allocation-free entry point does not create it).
+uint32_t* mailbox_word(DeviceState* ds, hipStream_t stream) {
+  if (!ds->mailbox_dev) return nullptr;
+  return ds->mailbox_dev + mailbox_slot(ds, stream);
+}
+
+// A timed-out exchange wait of an earlier call on `stream`, reported once.
+// Seen once that call's kernel has finished, so the first call on the stream
+// made after that (or wtc_check_status, which synchronises the stream first)
+// reports it.
+int take_mailbox(DeviceState* ds, hipStream_t stream) {  // no mailbox yet: nothing to report
+  if (!ds->mailbox_host) return WTC_OK;
+  uint32_t* word = const_cast<uint32_t*>(ds->mailbox_host) + mailbox_slot(ds, stream);
+  if (*word != 0u && __atomic_exchange_n(word, 0u, __ATOMIC_SEQ_CST) != 0u) {
     return fail(WTC_ERR_TIMEOUT,
-                "an exchange-path wait of an earlier call on this device timed out (its tiles "
+                "an exchange-path wait of an earlier call on this stream timed out (its tiles "
                 "were not all resident at once); that call's output is wrong");
+  }
+  return WTC_OK;
+}
+
+// Gives `stream`'s mailbox slot back (a timeout still in it is dropped).
+void release_slot(DeviceState* ds, hipStream_t stream) {
+  for (int i = 1; i < kMailboxSlots; ++i)
+    if (ds->slot_used[i] && ds->slot_stream[i] == stream) {
+      ds->slot_used[i] = false;
+      ds->slot_stream[i] = nullptr;
+      if (ds->mailbox_host) ds->mailbox_host[i] = 0u;
+    }
+}
+
+// Frees what the library holds for `stream` (its default workspace and the
+// buffers that one superseded) and gives its mailbox slot back.  The caller
+// has synchronised the stream; graphs captured on it that use its default
+// workspace must not be replayed afterwards.
+int release_stream_state(DeviceState* ds, hipStream_t stream) {
+  release_slot(ds, stream);
+  if (ds->exch_stream == stream) ds->exch_stream = nullptr;
+  for (size_t i = 0; i < ds->ws.size();) {
+    if (ds->ws[i].stream == stream) {
+      HIP_TRY(hipFree(ds->ws[i].ptr));
+      ds->ws.erase(ds->ws.begin() + (long)i);
+    } else {
+      ++i;
+    }
+  }
+  for (size_t i = 0; i < ds->retired.size();) {
+    if (ds->retired[i].stream == stream) {
+      HIP_TRY(hipFree(ds->retired[i].ptr));
+      ds->retired.erase(ds->retired.begin() + (long)i);
+    } else {
+      ++i;
+    }
   }
   return WTC_OK;
 }
@@ -565,7 +652,11 @@ int wtc_profile_tiles(int64_t batch, int64_t m, int64_t n, int64_t k, int in_dty
   hipStream_t st = nullptr;
   hipEvent_t e0 = nullptr, e1 = nullptr;
   auto release = [&]() {
-    if (st) (void)hipStreamSynchronize(st);
+    if (st) {
+      (void)hipStreamSynchronize(st);
+      std::lock_guard<std::mutex> lk(g_mu);
+      (void)release_stream_state(&g_dev[dev], st);
+    }
     for (void* q : {a, b, o, w})
       if (q) (void)hipFree(q);
     if (e0) (void)hipEventDestroy(e0);
@@ -608,7 +699,7 @@ int wtc_profile_tiles(int64_t batch, int64_t m, int64_t n, int64_t k, int in_dty
     std::lock_guard<std::mutex> lk(g_mu);
     DeviceState* ds = nullptr;
     r = device_state(dev, &ds);
-    return r ? r : take_mailbox(ds);
+    return r ? r : take_mailbox(ds, st);
   };
   rc = run();
   const std::string msg = g_last_error;
@@ -649,20 +740,43 @@ int wtc_workspace_init(void* workspace, size_t workspace_bytes, void* stream) {
 
 int wtc_set_exchange_wait_limit(uint64_t ticks) {
   g_last_error.clear();
-  g_spin_ticks.store(ticks ? ticks : kDefaultSpinTicks);
+  g_spin_ticks.store(ticks);
   return WTC_OK;
 }
 
-int wtc_check_status(void* stream) {
+int wtc_check_status(void* stream_) {
   g_last_error.clear();
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
   int dev = 0;
   HIP_TRY(hipGetDevice(&dev));
-  HIP_TRY(hipStreamSynchronize(static_cast<hipStream_t>(stream)));
+  HIP_TRY(hipStreamSynchronize(stream));
   std::lock_guard<std::mutex> lk(g_mu);
   DeviceState* ds = nullptr;
   int rc = device_state(dev, &ds);
   if (rc) return rc;
-  return take_mailbox(ds);
+  // the allocation-free entry point's set-up too, so that its calls after
+  // this one do none (they may then be captured into a graph)
+  void* scratch_ptr = nullptr;
+  rc = scratch_address(dev, &scratch_ptr);
+  if (rc) return rc;
+  return take_mailbox(ds, stream);
+}
+
+int wtc_release_stream(void* stream_) {
+  g_last_error.clear();
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  int dev = 0;
+  HIP_TRY(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxDevices) return fail(WTC_ERR_HIP, "device index out of range");
+  HIP_TRY(hipStreamSynchronize(stream));
+  std::lock_guard<std::mutex> lk(g_mu);
+  DeviceState* ds = &g_dev[dev];
+  const int rc = ds->mailbox_host ? take_mailbox(ds, stream) : WTC_OK;
+  const std::string msg = g_last_error;
+  const int frc = release_stream_state(ds, stream);
+  if (frc) return frc;
+  g_last_error = msg;
+  return rc;
 }
 
 int wtc_read_error_flags(void* workspace, uint32_t* flags, int clear) {
@@ -751,7 +865,7 @@ int matmul_softmax_impl(const void* a, const void* b, void* out, int64_t batch, 
   DeviceState* ds = nullptr;
   rc = device_state(dev, &ds, !noalloc);
   if (rc) return rc;
-  rc = take_mailbox(ds);
+  rc = take_mailbox(ds, stream);
   if (rc) return rc;
 
   Plan pl;
@@ -817,8 +931,8 @@ int matmul_softmax_impl(const void* a, const void* b, void* out, int64_t batch, 
   p.ent = reinterpret_cast<uint64_t*>(wsb + L.stats_off);
   p.gen = reinterpret_cast<uint32_t*>(wsb + L.gen_off);
   p.err = reinterpret_cast<uint32_t*>(wsb);
-  p.mailbox = ds->mailbox_dev;
-  p.spin_ticks = g_spin_ticks.load();
+  p.mailbox = mailbox_word(ds, stream);
+  p.spin_ticks = wait_limit_ticks(pl.est_us);
 
   const int cu_count = ds->cu_count;
   if (chosen != WTC_PATH_EXCHANGE) lk.unlock();
