@@ -50,7 +50,8 @@ _SIGS = {
     "wtc_ref_dequant_e4m3": (None, [_u8p, _f32p, _i64]),
     "wtc_ref_chain_rows": (ctypes.c_int, [_f32p, _f32p, _i64, _i64, _i64, _i64p, _i64,
                                           ctypes.c_double, _f64p, _f64p]),
-    "wtc_ref_chain_rows_f16acc": (ctypes.c_int, [_f32p, _f32p, _i64, _i64, _i64, _i64p, _i64, _f64p]),
+    "wtc_ref_chain_rows_f16acc": (ctypes.c_int, [_f32p, _f32p, _i64, _i64, _i64, _i64p, _i64,
+                                                  ctypes.c_float, _f64p]),
     "wtc_cpu_chain_loops_f32": (ctypes.c_double, [_f32p, _f32p, _f32p, _f32p, _i64, _i64, _i64,
                                                   _i64, ctypes.c_int]),
     "wtc_cpu_max_threads": (ctypes.c_int, []),
@@ -190,8 +191,9 @@ def chain_rows(a: np.ndarray, b: np.ndarray, rows, scale: float = 1.0):
     return logits, probs
 
 
-def chain_rows_f16acc(a: np.ndarray, b: np.ndarray, rows) -> np.ndarray:
-    """The reference lowering's f16-accumulate chain (information only)."""
+def chain_rows_f16acc(a: np.ndarray, b: np.ndarray, rows, scale: float = 1.0) -> np.ndarray:
+    """The reference lowering's f16-accumulate chain (information only):
+    f16 accumulation in k order, widened to f32, times `scale`, f32 softmax."""
     a = np.ascontiguousarray(a, np.float32)
     b = np.ascontiguousarray(b, np.float32)
     m, k = a.shape
@@ -199,7 +201,7 @@ def chain_rows_f16acc(a: np.ndarray, b: np.ndarray, rows) -> np.ndarray:
     rows = np.ascontiguousarray(np.asarray(rows, np.int64))
     probs = np.empty((rows.size, n), np.float64)
     rc = lib().wtc_ref_chain_rows_f16acc(_p(a, _f32p), _p(b, _f32p), m, n, k, _p(rows, _i64p),
-                                         rows.size, _p(probs, _f64p))
+                                         rows.size, float(scale), _p(probs, _f64p))
     if rc:
         raise ValueError("wtc_ref_chain_rows_f16acc failed")
     return probs

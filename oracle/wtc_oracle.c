@@ -348,11 +348,13 @@ WTC_EXPORT int wtc_ref_chain_rows(const float *A, const float *B, int64_t M,
  * f16 in k order, c = f16(c + f16(a*b)), from a zero fill
  * (bench/baselines/default/baseline/04c.after_linalg_to_loops.mlir:44-108,
  * mlir/matmul_softmax_chain_f16_native.mlir:13-17), widened to f32
- * (:21-31), then the f32 softmax.  Output in double. */
+ * (:21-31), times `scale` in f32 (a scaled chain such as attention's
+ * 1/sqrt(d) multiplies the widened logits; 1 for the reference's chain),
+ * then the f32 softmax.  Output in double. */
 WTC_EXPORT int wtc_ref_chain_rows_f16acc(const float *A, const float *B,
                                          int64_t M, int64_t N, int64_t K,
                                          const int64_t *rows, int64_t nrows,
-                                         double *out_probs) {
+                                         float scale, double *out_probs) {
   for (int64_t r = 0; r < nrows; ++r) {
     int64_t i = rows[r];
     if (i < 0 || i >= M)
@@ -364,6 +366,7 @@ WTC_EXPORT int wtc_ref_chain_rows_f16acc(const float *A, const float *B,
         float p = wtc_ref_f16_to_f32(wtc_ref_f32_to_f16(A[i * K + k] * B[k * N + j]));
         c = wtc_ref_f16_to_f32(wtc_ref_f32_to_f16(c + p));
       }
+      c *= scale;
       out_probs[r * N + j] = c;
       if (c > mx)
         mx = c;

@@ -49,6 +49,16 @@ def test_reference_named_libraries():
     assert hasattr(solver, "welder_solver_solve_typical_chain")
 
 
+def test_phase_stamps_only_in_the_profiling_build(L):
+    """The stamp reader exists only in libwtc_hip_stamps.so, which exports the
+    same C-ABI; the product library has no stamps."""
+    assert not hasattr(L, "wtc_phase_stamps_read")
+    S = _lib.stamps_lib()
+    assert hasattr(S, "wtc_phase_stamps_read")
+    for n in sorted(declared_functions()):
+        assert hasattr(S, n), n
+
+
 def test_version(L):
     assert b"gfx950" in L.wtc_version()
 

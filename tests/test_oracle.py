@@ -289,6 +289,11 @@ def test_f16_accumulate_variant_against_numpy_float16_loop():
     e = np.exp(c32 - c32.max(axis=1, keepdims=True))
     want = e / e.sum(axis=1, keepdims=True)
     np.testing.assert_allclose(got, want, rtol=2e-6, atol=1e-9)
+    # a scale multiplies the widened f16 logits before the softmax
+    got_s = O.chain_rows_f16acc(a, b, [0, 1, 2], scale=-0.375)
+    ys = c32 * np.float32(-0.375)
+    e = np.exp(ys - ys.max(axis=1, keepdims=True))
+    np.testing.assert_allclose(got_s, e / e.sum(axis=1, keepdims=True), rtol=2e-6, atol=1e-9)
 
 
 def test_cpu_loops_baseline_matches_chain():

@@ -97,6 +97,7 @@ SIGNATURES = {
 }
 
 _lib = None
+_stamps_lib = None
 
 
 class WtcError(RuntimeError):
@@ -105,29 +106,45 @@ class WtcError(RuntimeError):
         self.code = code
 
 
+def _load(path: Path) -> ctypes.CDLL:
+    if not path.exists():
+        raise RuntimeError(
+            f"{path} is missing: the HIP extension is not built "
+            "(run python -m welder_typical_chain_amd.build); no fallback exists")
+    # PyTorch ships its own HIP runtime (torch/lib/libamdhip64.so, soname
+    # libamdhip64.so.7) and asks for it as "libamdhip64.so".  Loaded first,
+    # it satisfies this library's libamdhip64.so.7 dependency, so one
+    # runtime serves both.  Loaded the other way round, the process would
+    # hold two HIP runtimes and the second one finds no device.
+    import torch  # noqa: F401
+    h = ctypes.CDLL(str(path))
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(h, name, None)
+        if fn is None:
+            continue
+        fn.restype = res
+        fn.argtypes = args
+    return h
+
+
 def lib() -> ctypes.CDLL:
     """The loaded library with every declared signature bound."""
     global _lib
     if _lib is None:
-        if not LIB_PATH.exists():
-            raise RuntimeError(
-                f"{LIB_PATH} is missing: the HIP extension is not built "
-                "(run python -m welder_typical_chain_amd.build); no fallback exists")
-        # PyTorch ships its own HIP runtime (torch/lib/libamdhip64.so, soname
-        # libamdhip64.so.7) and asks for it as "libamdhip64.so".  Loaded first,
-        # it satisfies this library's libamdhip64.so.7 dependency, so one
-        # runtime serves both.  Loaded the other way round, the process would
-        # hold two HIP runtimes and the second one finds no device.
-        import torch  # noqa: F401
-        h = ctypes.CDLL(str(LIB_PATH))
-        for name, (res, args) in SIGNATURES.items():
-            fn = getattr(h, name, None)
-            if fn is None:
-                continue
-            fn.restype = res
-            fn.argtypes = args
-        _lib = h
+        _lib = _load(LIB_PATH)
     return _lib
+
+
+def stamps_lib() -> ctypes.CDLL:
+    """The profiling build with the exchange kernel's phase stamps
+    (libwtc_hip_stamps.so): the same C-ABI plus wtc_phase_stamps_read."""
+    global _stamps_lib
+    if _stamps_lib is None:
+        h = _load(LIB_PATH.with_name("libwtc_hip_stamps.so"))
+        h.wtc_phase_stamps_read.restype = ctypes.c_int
+        h.wtc_phase_stamps_read.argtypes = [ctypes.POINTER(ctypes.c_int64), ctypes.c_int64]
+        _stamps_lib = h
+    return _stamps_lib
 
 
 def check(code: int) -> None:

@@ -6,6 +6,10 @@
   ``libwelder-solver-capi.so`` (CPU only: chain recogniser + tile solver): the
   file names the reference's toolchain looks for in its backend build
   directory (reference compiler/backend/Toolchain.cpp:29-45).
+- ``libwtc_hip_stamps.so``: the same library with the exchange kernel's
+  phase stamps compiled in (``-DWTC_PHASE_STAMPS``), for
+  ``python -m welder_typical_chain_amd.phase_timeline``; never loaded by the
+  product path.
 - ``wtc-compiler``: the reference's pipeline driver CLI (``--search-only``,
   ``--compile-only``, full) over the two C-ABIs, linked against
   ``libwtc_hip.so`` next to it.
@@ -30,6 +34,8 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 OBJ = PKG / "_build"
 LIB = PKG / "libwtc_hip.so"
+STAMPS_LIB = PKG / "libwtc_hip_stamps.so"
+STAMPS_SRC = "fused_matmul_softmax.hip"
 COMPILE_LIB = PKG / "libwelder-compile-capi.so"
 SOLVER_LIB = PKG / "libwelder-solver-capi.so"
 CLI = PKG / "wtc-compiler"
@@ -82,6 +88,13 @@ def _compile_one(src: str) -> Path:
         _run([HIPCC, *HIP_FLAGS, *HIP_EXTRA.get(src, []), "-c", str(path), "-o", str(obj)])
     else:
         _run(["g++", *CXX_FLAGS, "-c", str(path), "-o", str(obj)])
+    return obj
+
+
+def _compile_stamps() -> Path:
+    obj = OBJ / (STAMPS_SRC + ".stamps.o")
+    _run([HIPCC, *HIP_FLAGS, *HIP_EXTRA.get(STAMPS_SRC, []), "-DWTC_PHASE_STAMPS", "-c",
+          str(CSRC / STAMPS_SRC), "-o", str(obj)])
     return obj
 
 
@@ -190,11 +203,17 @@ def build(verbose: bool = False) -> Path:
     device_only = [s for s in HIP_SOURCES if s != "launch.hip"]
     with cf.ThreadPoolExecutor(max_workers=8) as ex:
         co_jobs = [ex.submit(_code_object, s) for s in device_only]
+        stamps_job = ex.submit(_compile_stamps)
         objs = list(ex.map(_compile_one, sources))
         code_objects = [j.result() for j in co_jobs]
+        stamps_obj = stamps_job.result()
     tmp = LIB.with_suffix(".so.tmp")
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-o", str(tmp), *map(str, objs)])
     os.replace(tmp, LIB)
+    stamps_objs = [stamps_obj if o.name == STAMPS_SRC + ".o" else o for o in objs]
+    tmp = STAMPS_LIB.with_suffix(".so.tmp")
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-o", str(tmp), *map(str, stamps_objs)])
+    os.replace(tmp, STAMPS_LIB)
     if COMPILE_LIB.is_symlink() or COMPILE_LIB.exists():
         COMPILE_LIB.unlink()
     COMPILE_LIB.symlink_to(LIB.name)

@@ -45,6 +45,31 @@
 
 namespace wtc {
 
+// Phase stamps, built only into the profiling library libwtc_hip_stamps.so
+// (WTC_PHASE_STAMPS): lane 0 of every wave of an exchange-path tile reads
+// the 100 MHz real-time counter at its phase boundaries, and at the end wave
+// 0 and the first loader wave write them to g_phase_stamps[tile][16]:
+//   0 start            1 k-tile 0 landed     2 K loop done
+//   3 wave statistics  4 entries published and acknowledged
+//   5 after the barrier that follows       6 tile staged (before the next)
+//   7 after it: the row block's table complete
+//   8 factors written  9 after the barrier that follows (generation stored)
+//   10 stores acknowledged
+//   11, 12 the shader-clock counter (s_memtime) at 1 and 2
+//   13, 14 the first loader wave's poll: start, end
+//   15 (row block << 8) | XCD
+// The stamps add no work to the kernel's phases (counter reads only).
+#if defined(WTC_PHASE_STAMPS)
+constexpr bool kPhaseStamps = true;
+#else
+constexpr bool kPhaseStamps = false;
+#endif
+constexpr int kStampWords = 16;
+constexpr int kStampTiles = 4096;
+#if defined(WTC_PHASE_STAMPS)
+__device__ int64_t g_phase_stamps[kStampTiles * kStampWords];
+#endif
+
 
 constexpr int BM = 128;
 constexpr int BN = 128;
@@ -610,6 +635,12 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
   const uint32_t rb = rbg - bt * nRB32;
   const int64_t row0 = rb * BM;
   const int64_t n0 = nt * BN;
+  [[maybe_unused]] uint64_t tlv[kStampWords] = {};
+  auto stamp = [&](int i) {
+    if constexpr (kPhaseStamps && EPI == kEpiExchange)
+      if (lane == 0) tlv[i] = __builtin_amdgcn_s_memrealtime();
+  };
+  stamp(0);
 
   constexpr int SZ = dtype_bytes(IN_DT);
   const int nk = (int)(((uint64_t)K32 * SZ + kKTileBytes - 1) / kKTileBytes);
@@ -692,6 +723,9 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
       }
       load_gen0();  // newer than the k-tile loads: only makes the waits below stricter
       wait_loads_barrier<LPT * (D - 1)>();  // k-tile 0 landed
+      stamp(1);
+      if constexpr (kPhaseStamps && EPI == kEpiExchange)
+        if (lane == 0) tlv[11] = __builtin_amdgcn_s_memtime();
       if (loader) {
         // Loader waves: the same waits and barriers as the MFMA waves, one
         // per k-tile; after each, k-tile kt+3 into the stage kt+3 % S.
@@ -736,6 +770,9 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
       }
       wait_loads_barrier<0>();
       }
+      stamp(2);
+      if constexpr (kPhaseStamps && EPI == kEpiExchange)
+        if (lane == 0) tlv[12] = __builtin_amdgcn_s_memtime();
     }
   } else if (nk == 0) {
     load_gen0();
@@ -864,6 +901,7 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
       if (lane < 32) wstat[wn * BM + wm * 64 + mt * 32 + jr] = make_float2(mx, sm);
     }
   }
+  stamp(3);
 
   // The tile's statistics of row r from the WN wave entries.
   auto tile_stat = [&](int r) {
@@ -905,6 +943,7 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
         // the wait, entries became visible to the other XCDs late on some
         // MI355X boxes (the exchange took 2-4 us longer), with it never.
         __builtin_amdgcn_s_waitcnt(0);
+        stamp(4);
       } else {
         // split: per-tile (max, sumexp) for the rescale kernel
         store_stat(p.partial + ((int64_t)rbg * BM + t) * p.nT + nt, st.x, st.y);
@@ -988,19 +1027,30 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
     // Loader waves poll as soon as this tile's entries are acknowledged,
     // while the MFMA waves stage the tile.
     __syncthreads();  // this tile's entry stores are acknowledged
-    if (!loader)
+    stamp(5);
+    if (!loader) {
       stage_tile();
-    else if (!solo)
+    } else if (!solo) {
+      stamp(13);
       poll_table(wave - C::kMfmaWaves, C::kWaves - C::kMfmaWaves);
+      stamp(14);
+    }
+    stamp(6);
     __syncthreads();  // the table and the staged tile are complete
+    stamp(7);
   } else {
     if (!loader) stage_tile();
+    stamp(6);
     if constexpr (EPI == kEpiExchange) {
       __syncthreads();  // the entries are acknowledged, the own log-sum-exps in the table
+      stamp(5);
       if (!solo) {
+        stamp(13);
         poll_table(wave, NT / 64);
+        stamp(14);
         __syncthreads();  // the table is complete
       }
+      stamp(7);
     }
   }
 
@@ -1066,12 +1116,14 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
       }
     }
   }
+  stamp(8);
   __syncthreads();
   // Every thread has its entries of the other slots: the next launch's
   // entries of this tile's slot may carry the next tag.
   if constexpr (EPI == kEpiExchange)
     if (t == 0 && !solo)
       __hip_atomic_store(p.gen + own_slot, sgen[nt] + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  stamp(9);
 
   // ---- scale, convert and store: 16 output bytes per thread per step -------
   // The exchange path writes final outputs that this launch never reads
@@ -1107,6 +1159,25 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
       }
     }
   }
+#if defined(WTC_PHASE_STAMPS)
+  if constexpr (EPI == kEpiExchange) {
+    __builtin_amdgcn_s_waitcnt(0);
+    stamp(10);
+    const int first_loader = LDW ? C::kMfmaWaves * 64 : 64;
+    if (blockIdx.x < (unsigned)kStampTiles && (t == 0 || t == first_loader)) {
+      int64_t* st = g_phase_stamps + (int64_t)blockIdx.x * kStampWords;
+      if (t == 0) {
+        uint32_t xcc;
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+        for (int i = 0; i <= 12; ++i) st[i] = (int64_t)tlv[i];
+        st[15] = ((int64_t)rbg << 8) | (xcc & 0xF);
+      } else {
+        st[13] = (int64_t)tlv[13];
+        st[14] = (int64_t)tlv[14];
+      }
+    }
+  }
+#endif
 }
 
 // -------------------------------------------------------------------------
@@ -1339,3 +1410,14 @@ int chain_kernel_lds_bytes(int in_dt, int out_dt, int loaders) {
 }
 
 }  // namespace wtc
+
+#if defined(WTC_PHASE_STAMPS)
+// Copies the phase stamps of tiles [0, tiles) of the last exchange launch
+// (int64 [tiles][16], layout above) to host memory; synchronous.
+extern "C" int wtc_phase_stamps_read(int64_t* host, int64_t tiles) {
+  if (!host || tiles <= 0 || tiles > wtc::kStampTiles) return 1;
+  const size_t bytes = (size_t)tiles * wtc::kStampWords * sizeof(int64_t);
+  return hipMemcpyFromSymbol(host, HIP_SYMBOL(wtc::g_phase_stamps), bytes, 0,
+                             hipMemcpyDeviceToHost) == hipSuccess ? 0 : 3;
+}
+#endif
