@@ -48,6 +48,9 @@ def parse():
     ap.add_argument("--workload", default="C2", choices=["C2", "C3", "C4", "C5"],
                     help="C2 is the headline; C3-C5 are the other BASELINE.json configurations, "
                          "timed the same way (no cpu_baseline)")
+    ap.add_argument("--vendor-gemm", action="store_true",
+                    help="also time the vendor GEMM alone (torch.matmul / bmm on hipBLASLt; fp8: "
+                         "torch._scaled_mm) on the same inputs, as context (\"vendor_gemm\")")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="before the timed steps, run plain device copies of this many MiB "
                          "(the byte-count calibration for rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -118,6 +121,47 @@ def cpu_baseline(a_host, b_host, n, k, budget_s):
 
 PEAKS = {"f16": PEAK_F16_TFLOPS, "bf16": PEAK_F16_TFLOPS, "fp8": 5000.0}
 TORCH_DT = {"f16": "float16", "bf16": "bfloat16", "fp8": "float8_e4m3fn", "f32": "float32"}
+
+
+def vendor_gemm(a, b, scale_a, scale_b, out_dtype, steps, torch):
+    """The same product A.B alone (no softmax) through PyTorch's GEMM, which
+    dispatches to hipBLASLt: torch.matmul (batched: bmm on contiguous
+    operands), fp8 e4m3 through torch._scaled_mm with the per-tensor scales
+    (its second operand column-major, as it requires).  HIP events over
+    `steps` back-to-back calls after 20 warmups; context only."""
+    if a.dtype == torch.float8_e4m3fn:
+        bt = b.t().contiguous().t()
+        sa = torch.tensor(scale_a, dtype=torch.float32, device=a.device)
+        sb = torch.tensor(scale_b, dtype=torch.float32, device=a.device)
+        op = "torch._scaled_mm (hipBLASLt, fp8 e4m3, per-tensor scales)"
+
+        def f():
+            return torch._scaled_mm(a, bt, scale_a=sa, scale_b=sb, out_dtype=out_dtype)
+    elif a.dim() == 3:
+        op = "torch.bmm (hipBLASLt)"
+
+        def f():
+            return torch.bmm(a, b)
+    else:
+        op = "torch.matmul (hipBLASLt)"
+
+        def f():
+            return torch.matmul(a, b)
+    for _ in range(20):
+        f()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        f()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / steps
+    m, k = a.shape[-2], a.shape[-1]
+    flops = 2 * (a.shape[0] if a.dim() == 3 else 1) * m * b.shape[-1] * k
+    return {"op": op, "us_per_call": round(us, 2), "tflops": round(flops / (us * 1e-6) / 1e12, 1),
+            "note": "the GEMM alone, without the softmax; context, not the metric"}
 
 
 def make_workload(cfg, dev, torch):
@@ -273,6 +317,10 @@ def main():
     row_dev = float((out.float().sum(-1) - 1).abs().max()) if out.numel() <= (1 << 28) else \
         float((out[..., :256, :].float().sum(-1) - 1).abs().max())
 
+    vendor = None
+    if args.vendor_gemm:
+        vendor = vendor_gemm(a, b, scale_a, scale_b, out_dt, min(args.steps, 50), torch)
+
     cpu = None
     if args.cpu_seconds > 0 and headline:
         cpu = cpu_baseline(a.float().cpu().numpy(), b.float().cpu().numpy(), n, k, args.cpu_seconds)
@@ -303,6 +351,8 @@ def main():
             "launch": launch_info,
             "checks": {"row_sum_max_dev": row_dev, "device_error_flags": flags},
         }
+        if vendor:
+            line["vendor_gemm"] = vendor
         print(json.dumps(line), flush=True)
         return
 
@@ -330,6 +380,8 @@ def main():
         "checks": {"row_sum_max_dev": row_dev, "device_error_flags": flags,
                    "host_wall_s_timed_region": round(t_host, 4)},
     }
+    if vendor:
+        line["vendor_gemm"] = vendor
     print(json.dumps(line), flush=True)
 
 
