@@ -85,7 +85,7 @@ def test_variant_parity(native_lib, in_dtype, out_dtype, variant, tiles, path, s
         err = logit_error_bound(inp.a[bt], inp.b[bt], rows, inp.scale, logits, in_dtype)
         compare_rows(out_np[bt], probs, logits, out_dtype, label=f"{variant} {path} batch {bt}",
                      in_dtype=in_dtype, logit_err=err)
-    check_row_sums(out, f"{variant} {path}", roundings=2 if path == "split" else 1)
+    check_row_sums(out, f"{variant} {path}", split=path == "split")
 
 
 @needs_gpu

@@ -18,6 +18,15 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 constexpr uint32_t kOutOfRange = 0x80000000u;  // buffer offset that reads 0
+// The split path's first pass stores exp2(y - tile max) (in [0, 1]) for
+// the rescale pass to scale in place: in the output type, except that a
+// bf16 output keeps them in f16 (the same 2 bytes, 2^-11 instead of 2^-8
+// rounding), so that the output is rounded to bf16 only once, by the
+// rescale pass.  Those f16 values are stored times 2^15 (exact), so that
+// exponentials down to 2^-29 keep f16's full precision and only those
+// below 2^-39 flush to zero; the rescale factor carries the 2^-15 back.
+constexpr int split_store_dt(int out_dt) { return out_dt == DT_BF16 ? DT_F16 : out_dt; }
+constexpr float split_store_scale(int out_dt) { return out_dt == DT_BF16 ? 32768.0f : 1.0f; }
 template <int OUT_DT> struct OutTraits;
 template <> struct OutTraits<DT_F32> { static constexpr int SZ = 4; };
 template <> struct OutTraits<DT_F16> { static constexpr int SZ = 2; };

@@ -1079,6 +1079,10 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
   // rescale kernel and stay ordinary stores (non-temporal ones cost 6 % there).
   uint8_t* o_base = p.out + bt * p.o_bstride;
   constexpr int OSZ = OutTraits<OUT_DT>::SZ;
+  // The type the tile's outputs are stored in: the split path keeps its
+  // intermediate exponentials (rescaled in place afterwards) in f16 when the
+  // output is bf16, so that a bf16 output is rounded to bf16 once.
+  constexpr int kStoreDt = EPI == kEpiSplit ? split_store_dt(OUT_DT) : OUT_DT;
   constexpr int EPC = 16 / OSZ;       // elements per 16-byte chunk
   constexpr int CPR = BN / EPC;       // chunks per tile row
   auto store16 = [](uint8_t* dst, const u32x4& v) {
@@ -1093,15 +1097,17 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
     const int64_t m = row0 + row;
     const int64_t n = n0 + ch * EPC;
     if (m < p.M && n < p.N) {
-      const float f = EPI == kEpiLogits ? 1.0f : factor[(ch * EPC / (32 * NTN)) * BM + row];
+      const float f = EPI == kEpiLogits ? 1.0f
+                      : factor[(ch * EPC / (32 * NTN)) * BM + row] *
+                            (EPI == kEpiSplit ? split_store_scale(OUT_DT) : 1.0f);
       const float* src = stg + row * kStagePitch + ch * EPC;
       if constexpr (OSZ == 4) {
         const f32x4 x0 = *reinterpret_cast<const f32x4*>(src) * f;
         store16(o_base + m * p.ldo_bytes + n * OSZ, __builtin_bit_cast(u32x4, x0));
       } else {
         uint32_t w0, w1, w2, w3;
-        pack4_product<OUT_DT>(*reinterpret_cast<const f32x4*>(src), f, &w0, &w1);
-        pack4_product<OUT_DT>(*reinterpret_cast<const f32x4*>(src + 4), f, &w2, &w3);
+        pack4_product<kStoreDt>(*reinterpret_cast<const f32x4*>(src), f, &w0, &w1);
+        pack4_product<kStoreDt>(*reinterpret_cast<const f32x4*>(src + 4), f, &w2, &w3);
         store16(o_base + m * p.ldo_bytes + n * OSZ, u32x4{w0, w1, w2, w3});
       }
     }
@@ -1165,7 +1171,7 @@ rescale_rows_kernel(uint8_t* __restrict__ out, const float2* __restrict__ partia
     for (int q = lane; q < nT; q += 64) gs += st[q].y * __builtin_amdgcn_exp2f(st[q].x - gm);
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) gs += __shfl_xor(gs, off);
-    const float inv = 1.0f / gs;
+    const float inv = 1.0f / gs / split_store_scale(OUT_DT);  // the stored values' scale removed
     for (int q = lane; q < nT; q += 64) fac[w][q] = __builtin_amdgcn_exp2f(st[q].x - gm) * inv;
   }
   __syncthreads();
@@ -1189,9 +1195,12 @@ rescale_rows_kernel(uint8_t* __restrict__ out, const float2* __restrict__ partia
         y = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x0) |
             ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x1) << 16);
       } else {
-        const uint32_t lo = x << 16, hi = x & 0xFFFF0000u;
-        const float x0 = __builtin_bit_cast(float, lo) * f;
-        const float x1 = __builtin_bit_cast(float, hi) * f;
+        // bf16 output: the tile kernel left its exponentials in f16
+        // (split_store_dt), rounded to bf16 once here
+        static_assert(split_store_dt(DT_BF16) == DT_F16, "bf16 outputs stage f16 exponentials");
+        const uint16_t lo = (uint16_t)(x & 0xFFFFu), hi = (uint16_t)(x >> 16);
+        const float x0 = (float)__builtin_bit_cast(_Float16, lo) * f;
+        const float x1 = (float)__builtin_bit_cast(_Float16, hi) * f;
         y = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x0) |
             ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x1) << 16);
       }

@@ -358,7 +358,8 @@ chain_wide_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
   // (sched_barrier keeps the subtiles apart), so at most 64 of them are in
   // VGPRs at once.  Split path: pass 1 takes each row's max over the tile
   // (per wave, then the two waves of a row through LDS); pass 2 writes
-  // exp2(y - tile max) in the output type into the staging area and sums it.
+  // exp2(y - tile max) into the staging area (in the output type; bf16
+  // outputs: f16 times 2^15, split_store_dt) and sums it.
   const int jr = acc_j(lane);
   float* wred = reinterpret_cast<float*>(smem + L::RED_OFF);  // [2][kTM] wave max, then wave sum
   float* tmax = wred + 2 * kTM;                               // [kTM] tile max per row
@@ -370,7 +371,10 @@ chain_wide_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
       *reinterpret_cast<f32x4*>(dst) = x;
     } else {
       uint32_t w0, w1;
-      pack4<OUT_DT>(x, &w0, &w1);
+      if constexpr (EPI == kEpiSplit)
+        pack4<split_store_dt(OUT_DT)>(x * split_store_scale(OUT_DT), &w0, &w1);
+      else
+        pack4<OUT_DT>(x, &w0, &w1);
       *reinterpret_cast<u32x2*>(dst) = u32x2{w0, w1};
     }
   };
