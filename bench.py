@@ -44,10 +44,11 @@ def parse():
                          "steady state; a 10-step warmup times the first loop 2-5 %% slow)")
     ap.add_argument("--path", default="auto", choices=["auto", "exchange", "split", "unfused", "rows"])
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
-                    help="budget of the cpu_baseline sample (0 disables it)")
+                    help="budget of the cpu_baseline sample (0 disables it); C3-C5 time a row "
+                         "sample of batch 0 and extrapolate")
     ap.add_argument("--workload", default="C2", choices=["C2", "C3", "C4", "C5"],
                     help="C2 is the headline; C3-C5 are the other BASELINE.json configurations, "
-                         "timed the same way (no cpu_baseline)")
+                         "timed the same way (their cpu_baseline extrapolates a row sample)")
     ap.add_argument("--vendor-gemm", action="store_true",
                     help="also time the vendor GEMM alone (torch.matmul / bmm on hipBLASLt; fp8: "
                          "torch._scaled_mm) on the same inputs, as context (\"vendor_gemm\")")
@@ -117,6 +118,35 @@ def cpu_baseline(a_host, b_host, n, k, budget_s):
                               "c2_full_s_extrapolated": round(secs1 * rows_total / rows1, 2)},
             "c1_full_us": {**c1_us, "flop": c1.flops,
                            "problem": "C1 f32 128x128 . 128x128, uniform[-1,1], seed 0"}}
+
+
+def cpu_baseline_sample(cfg, a_host, b_host, budget_s):
+    """C3-C5: the same f32 loop nest (inputs widened to f32: fp8 decoded and
+    scaled) on a sample of batch 0's first rows, on all `nproc` cores and on
+    one core, each extrapolated linearly to the whole problem (batch x M
+    rows), as labelled.  The logit scale is left out: it does not change
+    the loops' time."""
+    from oracle import oracle as O
+    host = host_info()
+    threads = max(1, host["nproc"])
+    n, k = cfg.n, cfg.k
+    rows_total = cfg.batch * cfg.m
+    _, t_cal = O.cpu_chain_loops(a_host, b_host, 0, threads, threads, baseline=True)
+    per_row_all = max(t_cal / threads, 1e-9)
+    rows = min(cfg.m, max(threads, int(budget_s / 2 / per_row_all) // threads * threads))
+    _, secs = O.cpu_chain_loops(a_host, b_host, 0, rows, threads, baseline=True)
+    _, t_one = O.cpu_chain_loops(a_host, b_host, 0, 1, 1, baseline=True)
+    rows1 = min(cfg.m, max(2, int(budget_s / 3 / max(t_one, 1e-9))))
+    _, secs1 = O.cpu_chain_loops(a_host, b_host, 0, rows1, 1, baseline=True)
+    return {"value": round(2.0 * rows * n * k / secs / 1e12, 6), "unit": "TFLOP/s", "cores": threads,
+            "kind": "port",
+            "sample": (f"{cfg.name} rows 0..{rows - 1} of batch 0 (f32 i-j-k loops + max/exp/sum/div, "
+                       f"OpenMP over rows on {threads} threads), {secs:.2f} s"),
+            "full_s_extrapolated": round(secs * rows_total / rows, 2),
+            "compiler": "ROCm clang -O3 -fopenmp (LLVM CPU backend)", "host": host,
+            "single_thread": {"value": round(2.0 * rows1 * n * k / secs1 / 1e12, 6), "cores": 1,
+                              "sample": f"{cfg.name} {rows1} rows, {secs1:.2f} s",
+                              "full_s_extrapolated": round(secs1 * rows_total / rows1, 2)}}
 
 
 PEAKS = {"f16": PEAK_F16_TFLOPS, "bf16": PEAK_F16_TFLOPS, "fp8": 5000.0}
@@ -324,6 +354,11 @@ def main():
     cpu = None
     if args.cpu_seconds > 0 and headline:
         cpu = cpu_baseline(a.float().cpu().numpy(), b.float().cpu().numpy(), n, k, args.cpu_seconds)
+    elif args.cpu_seconds > 0:
+        a0 = (a[0] if a.dim() == 3 else a).float() * scale_a
+        b0 = (b[0] if b.dim() == 3 else b).float() * scale_b
+        cpu = cpu_baseline_sample(cfg, a0.cpu().numpy(), b0.cpu().numpy(), args.cpu_seconds)
+        del a0, b0
 
     peak = PEAKS[cfg.in_dtype]
     traffic, traffic_src = load_traffic(args.workload, args.path)
@@ -348,6 +383,7 @@ def main():
                          {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
                           "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
                           "traffic": traffic, "traffic_profile": traffic_src}),
+            "cpu_baseline": cpu,
             "launch": launch_info,
             "checks": {"row_sum_max_dev": row_dev, "device_error_flags": flags},
         }
