@@ -1140,9 +1140,9 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
 // enough waves); wave `part` of a row takes its 16-byte chunks part, part +
 // wpr, ... in steps of 64 lanes.  Every wave merges the row's nT tile
 // statistics into (max, sum) itself, then rescales its chunks of the
-// tile-relative exponentials in place: out *= exp2(m_t - M) / S.  Four
-// chunks per lane are loaded before any is stored, so each lane keeps four
-// loads in flight.
+// tile-relative exponentials in place: out *= exp2(m_t - M) / S.  Eight
+// chunks per lane are loaded before any is stored, so each lane keeps eight
+// loads in flight (C5: 36.3 -> 35.1 us against four; C4 unchanged).
 // -------------------------------------------------------------------------
 template <int OUT_DT>
 __global__ void __launch_bounds__(256)
@@ -1150,7 +1150,7 @@ rescale_rows_kernel(uint8_t* __restrict__ out, const float2* __restrict__ partia
                     int64_t rows_total, int64_t M, int64_t rows_pad, int64_t N,
                     int64_t ldo_bytes, int64_t o_bstride, int nT, int tshift, int wpr) {
   constexpr int MAX_NT = 512;
-  constexpr int U = 4;  // chunks in flight per lane
+  constexpr int U = 8;  // chunks in flight per lane
   __shared__ float fac[4][MAX_NT];
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t gw = (int64_t)blockIdx.x * 4 + w;  // global wave
