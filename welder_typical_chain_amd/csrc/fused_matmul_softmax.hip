@@ -813,39 +813,59 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
             acc[mt][j][v] = n_loc < nvalid ? (zero ? 0.0f : acc[mt][j][v]) : pad;
           }
     }
-    const bool neg = c2 < 0.0f;  // wave-uniform
+    // Both m-subtiles in one block of straight-line code, with the sign of
+    // the scale resolved by one uniform branch around it, so that the
+    // scheduler interleaves the two subtiles' reductions and exponentials;
+    // each extreme is taken over four independent partial extremes (a max
+    // does not depend on the order, so the result is the same).
+    auto stats = [&](auto neg_c) {
+      constexpr bool NEG = decltype(neg_c)::value;
+      auto pick = [](float a, float b) { return NEG ? fminf(a, b) : fmaxf(a, b); };
+      // partial extremes per subtile (one on the 256-row layout, whose
+      // waves have no registers to spare)
+      constexpr int PX = TM == 256 ? 1 : 4;
+      float ext[2];
 #pragma unroll
-    for (int mt = 0; mt < (loader ? 0 : 2); ++mt) {
-      // the row's extreme accumulator over the wave's columns (lane l and
-      // l ^ 32 hold the two halves of the row)
-      float ext = acc[mt][0][0];
-      if (neg) {
+      for (int mt = 0; mt < 2; ++mt) {
+        // the row's extreme accumulator over the wave's columns (lane l and
+        // l ^ 32 hold the two halves of the row)
+        float ex[PX];
+#pragma unroll
+        for (int i = 0; i < PX; ++i) ex[i] = acc[mt][0][i];
 #pragma unroll
         for (int j = 0; j < NTN; ++j)
 #pragma unroll
-          for (int v = 0; v < 16; ++v) ext = fminf(ext, acc[mt][j][v]);
-        ext = xor32_min(ext);
-      } else {
+          for (int v = 0; v < 16; ++v)
+            if (j > 0 || v >= PX) ex[v % PX] = pick(ex[v % PX], acc[mt][j][v]);
+        ext[mt] = ex[0];
 #pragma unroll
-        for (int j = 0; j < NTN; ++j)
-#pragma unroll
-          for (int v = 0; v < 16; ++v) ext = fmaxf(ext, acc[mt][j][v]);
-        ext = xor32_max(ext);
+        for (int i = 1; i < PX; ++i) ext[mt] = pick(ext[mt], ex[i]);
       }
-      // max of y; -inf when every column of the wave lies past N (pad * c2)
-      const float mx = ext * c2;
-      const float nbase = mx == -INFINITY ? 0.0f : -mx;
-      float s4[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // independent partial sums
 #pragma unroll
-      for (int j = 0; j < NTN; ++j)
+      for (int mt = 0; mt < 2; ++mt) ext[mt] = NEG ? xor32_min(ext[mt]) : xor32_max(ext[mt]);
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[mt][j][v], c2, nbase));
-          acc[mt][j][v] = e;
-          s4[v & 3] += e;
-        }
-      const float sm = xor32_sum((s4[0] + s4[1]) + (s4[2] + s4[3]));
-      if (lane < 32) wstat[wn * BM + wm * 64 + mt * 32 + jr] = make_float2(mx, sm);
+      for (int mt = 0; mt < 2; ++mt) {
+        // max of y; -inf when every column of the wave lies past N (pad * c2)
+        const float mx = ext[mt] * c2;
+        const float nbase = mx == -INFINITY ? 0.0f : -mx;
+        float s4[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // independent partial sums
+#pragma unroll
+        for (int j = 0; j < NTN; ++j)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[mt][j][v], c2, nbase));
+            acc[mt][j][v] = e;
+            s4[v & 3] += e;
+          }
+        const float sm = xor32_sum((s4[0] + s4[1]) + (s4[2] + s4[3]));
+        if (lane < 32) wstat[wn * BM + wm * 64 + mt * 32 + jr] = make_float2(mx, sm);
+      }
+    };
+    if (!loader) {
+      if (c2 < 0.0f)
+        stats(std::true_type{});
+      else
+        stats(std::false_type{});
     }
   }
   stamp(3);
