@@ -25,6 +25,15 @@ pytestmark = pytest.mark.gpu
 needs_gpu = pytest.mark.skipif(not torch.cuda.is_available(), reason="no GPU")
 
 
+# K of the timeout tests.  A wait runs out only when a tile's first poll
+# misses an entry, i.e. when the tiles of a row block publish further apart
+# than a tile takes to publish its own; that spread grows with the K loop.
+# Measured on MI355X at M = N = 2048 with a 2-tick limit: K = 256 timed out
+# in 0 of 30 calls on one box, K = 1024 in 22 of 30, K = 4096 in 30 of 30
+# (hundreds of timed-out waits per call).
+K_TIMEOUT = 4096
+
+
 def _announce(msg: str) -> None:
     print(f"\n[gpu-case] {msg}", flush=True)
 
@@ -45,14 +54,14 @@ def test_exchange_timeout_is_reported(native_lib):
                                                 workspace_size)
     _announce("exchange wait limit of 2 ticks: timeouts reported, then a clean call")
     m = n = 2048
-    k = 256
+    k = K_TIMEOUT
     a, b = _inputs(m, n, k, 3)
     ws = new_workspace(workspace_size(1, m, n, k, 1, 1, "exchange"))
     ref = torch.softmax(a.float() @ b.float(), dim=-1)
     try:
         set_exchange_wait_limit(2)  # 20 ns: tiles that finish first give up
         reported = False
-        for _ in range(3):
+        for _ in range(8):
             matmul_softmax(a, b, path="exchange", workspace=ws)
             try:
                 check_status()
@@ -100,7 +109,7 @@ def test_timeout_is_reported_to_its_own_stream(native_lib):
                                                 set_exchange_wait_limit, workspace_size)
     _announce("two streams: A times out at a 2-tick limit, B runs, A's next call reports")
     m = n = 2048
-    k = 256
+    k = K_TIMEOUT
     a, b = _inputs(m, n, k, 5)
     ref = torch.softmax(a.float() @ b.float(), dim=-1)
     nbytes = workspace_size(1, m, n, k, 1, 1, "exchange")
