@@ -298,12 +298,20 @@ chain_wide_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
+          // each load right behind an MFMA, so that the matrix core has work
+          // while the wave waits for the memory pipeline to take the load
+          mma16<IN_DT>(p1, g, 0, acc);
+          __builtin_amdgcn_sched_barrier(0);
           d.issue_one(fill, kt + kStages, 2 * g);
+          __builtin_amdgcn_sched_barrier(0);
+          mma16<IN_DT>(p1, g, 1, acc);
+          __builtin_amdgcn_sched_barrier(0);
           d.issue_one(fill, kt + kStages, 2 * g + 1);
+          __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
           for (int u = 0; u < 3; ++u) read16(nxt, fb, 0, 3 * g + u, p0);
-#pragma unroll
-          for (int nt = 0; nt < 4; ++nt) mma16<IN_DT>(p1, g, nt, acc);
+          mma16<IN_DT>(p1, g, 2, acc);
+          mma16<IN_DT>(p1, g, 3, acc);
           __builtin_amdgcn_sched_barrier(0);
         }
       }
@@ -334,10 +342,15 @@ chain_wide_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int g = 0; g < 4; ++g) {  // m-subtile g, n-subtiles 2, 3; then its next A
-          d.issue_one(fill, kt + kStages, 2 * g);
-          d.issue_one(fill, kt + kStages, 2 * g + 1);
+          // each load right behind an MFMA (as in the 16-bit loop)
           mma8(pa.a[g], pb.b[0], acc[g][2]);
+          __builtin_amdgcn_sched_barrier(0);
+          d.issue_one(fill, kt + kStages, 2 * g);
+          __builtin_amdgcn_sched_barrier(0);
           mma8(pa.a[g], pb.b[1], acc[g][3]);
+          __builtin_amdgcn_sched_barrier(0);
+          d.issue_one(fill, kt + kStages, 2 * g + 1);
+          __builtin_amdgcn_sched_barrier(0);
           read8_a(nxt, fb, g, pa);
 #pragma unroll
           for (int u = 0; u < 2; ++u) {
