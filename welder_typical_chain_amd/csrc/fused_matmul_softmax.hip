@@ -54,9 +54,7 @@ namespace wtc {
 //   3 wave statistics  4 entries published and acknowledged
 //   5 after the barrier that follows       6 tile staged (before the next)
 //   7 after it: the row block's table complete
-//   8 factors written  9 after the wait that follows (a barrier where the
-//                        stores are not made by the rows' own quads;
-//                        generation stored)
+//   8 factors written  9 after the barrier that follows (generation stored)
 //   10 stores acknowledged
 //   11, 12 the shader-clock counter (s_memtime) at 1 and 2
 //   13, 14 the first loader wave's poll: start, end

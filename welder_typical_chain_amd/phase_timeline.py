@@ -37,7 +37,7 @@ PHASES = [
     ("loader poll", 14, 13, "first loader wave polls the row block's entries"),
     ("barrier B", 7, 6, "wave 0 waits for the table (the loaders' poll)"),
     ("merge", 8, 7, "row log-sum-exp from the table, factors to LDS"),
-    ("factor wait", 9, 8, "the wave's factors in LDS (no barrier), generation stored"),
+    ("barrier C", 9, 8, "factors in place, generation stored"),
     ("stores", 10, 9, "scale, convert, 16-byte stores, acknowledged"),
     ("tile total", 10, 0, "start -> stores acknowledged"),
 ]
