@@ -1084,14 +1084,7 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
     }
   }
   stamp(8);
-  // exchange path, 4 threads per row: each row's quad stores the row itself
-  // (below), so its factors -- written by lanes of the same wave -- need only
-  // this wave's LDS writes complete, not a barrier
-  constexpr bool kQuadStores = EPI == kEpiExchange && NT / BM == 4;
-  if constexpr (kQuadStores)
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-  else
-    __syncthreads();
+  __syncthreads();
   // Every thread has its entries of the other slots: the next launch's
   // entries of this tile's slot may carry the next tag.
   if constexpr (EPI == kEpiExchange)
@@ -1120,10 +1113,7 @@ chain_tile_kernel(const uint8_t* a_in, const uint8_t* b_in, uint32_t M32, uint32
   };
 #pragma unroll 4
   for (int idx = t; idx < BM * CPR; idx += NT) {
-    // quad stores: thread (r, h) = (t / 4, t % 4) takes chunks h, h + 4, ...
-    // of row r; otherwise consecutive threads take consecutive chunks
-    const int row = kQuadStores ? t / 4 : idx / CPR;
-    const int ch = kQuadStores ? (t % 4) + 4 * ((idx - t) / NT) : idx % CPR;
+    const int row = idx / CPR, ch = idx % CPR;
     const int64_t m = row0 + row;
     const int64_t n = n0 + ch * EPC;
     if (m < p.M && n < p.N) {
