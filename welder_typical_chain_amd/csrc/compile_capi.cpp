@@ -182,7 +182,7 @@ static std::string emit_loop_structure(const ChainSpec& spec, const VariantDesc&
       o << "      // one 128-row block over all of N; A staged in LDS once\n"
         << "      scf.for %pass = %c0 to %c2 step %c1 {  // pass 0: online row max/sum; pass 1: "
            "exp2(y - max - log2 sum) stored\n"
-        << "        scf.for %t = %c0 to %nT step %c1 {  // 128-column B tiles through a 4-stage "
+        << "        scf.for %t = %c0 to %nT step %c1 {  // 128-column B tiles through a 3-stage "
            "direct-to-LDS ring\n"
         << "          scf.for %s = %c0 to %ks step %c1 {  // " << mfma << "\n          }\n"
         << "        }\n      }\n";

@@ -18,6 +18,8 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 constexpr uint32_t kOutOfRange = 0x80000000u;  // buffer offset that reads 0
+// cache-policy operand of the buffer builtins on gfx950: the nt bit
+constexpr int kCachePolicyNT = 2;
 // The split path's first pass stores exp2(y - tile max) (in [0, 1]) for
 // the rescale pass to scale in place: in the output type, except that a
 // bf16 output keeps them in f16 (the same 2 bytes, 2^-11 instead of 2^-8

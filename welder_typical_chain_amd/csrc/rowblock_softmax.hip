@@ -6,8 +6,8 @@
 // MFMAs, so each workgroup computes its logits twice instead of exchanging
 // row statistics with other workgroups or rescaling a stored output:
 //   pass 1: for every 128-column tile, A.B on MFMA, online row max / sum of
-//           exp2 in registers (each wave over its 64 columns of every tile),
-//           merged across the 2 column-waves through LDS at the end;
+//           exp2 in registers (each wave over its 32 columns of every tile),
+//           merged across the 4 column-waves through LDS at the end;
 //   pass 2: the same products again, out = exp2(y - max) / sum, stored once.
 // The output is written exactly once and nothing else goes to HBM (no
 // workspace).  The row block's A goes to LDS once and its MFMA fragments stay
@@ -15,18 +15,20 @@
 // LDS ring of direct-to-LDS loads (the same K-major, XOR-swizzled B layout
 // and transpose reads as chain_tile_kernel).
 //
-// 8 waves in two roles, one of each per SIMD:
-//   compute waves 0-3, 2 x 2: wave (wm, wn) owns rows wm*64 .. +63 and
-//     columns wn*64 .. +63 of each tile (2 x 2 MFMA subtiles of 32 x 32); they
-//     issue no global memory instruction for 16-bit outputs: the MFMAs, the
-//     softmax arithmetic and LDS traffic only;
-//   I/O waves 4-7: the row block's A, every B tile load, and the output
+// 12 waves in two roles, three per SIMD:
+//   compute waves 0-7, 2 x 4: wave (wm, wn) owns rows wm*64 .. +63 and
+//     columns wn*32 .. +31 of each tile (two 32 x 32 MFMA subtiles); waves w
+//     and w + 4 share a SIMD.  For 16-bit outputs they issue no global
+//     memory instruction: the MFMAs, the softmax arithmetic and LDS traffic;
+//   I/O waves 8-11: the row block's A, every B tile load, and the output
 //     stores: 16-bit outputs reach them through an LDS out stage (two, one
 //     per tile parity), from which each store instruction writes 4 whole
-//     256-byte row segments (full 128-byte lines).
-// A compute wave that issued its own loads and stores waited for the memory
-// pipeline to take each of them while its SIMD's matrix core sat idle; here
-// the I/O wave of the SIMD waits instead.  f32 outputs (a 64 KiB tile) are
+//     256-byte row segments (full 128-byte lines, non-temporal).
+// A wave that issues a load or store waits until the memory pipeline takes
+// it; with the I/O waves doing so, the compute waves keep the matrix cores
+// and the VALU busy, and with two compute waves per SIMD one issues its
+// softmax arithmetic while the other's MFMAs run (one wave alone issues
+// VALU work well below the SIMD's rate).  f32 outputs (a 64 KiB tile) are
 // stored by the compute waves from registers.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -43,7 +45,8 @@ namespace rows {
 
 constexpr int BM = 128;             // rows per workgroup
 constexpr int BN = 128;             // columns per tile
-constexpr int NT = 512;             // threads: 4 compute waves, then 4 I/O waves
+constexpr int NCW = 8;             // compute waves, 2 x 4 (64 x 32 each)
+constexpr int NT = 64 * (NCW + 4);  // threads: 8 compute waves, then 4 I/O waves
 constexpr int KS = 8;               // k-steps of 16: K <= 128
 constexpr int A_KT = KS / 4;        // A k-tiles of 64 elements (128 bytes) per row
 constexpr int A_BYTES = A_KT * BM * 128;  // the row block's A, 32 KiB
@@ -60,7 +63,7 @@ constexpr int SPW = BM / 4 / 4;     // store instructions per I/O wave and tile 
 constexpr int LDS_BYTES = RING_OFF + S * STAGE;  // 160 KiB
 static_assert(LDS_BYTES <= 160 * 1024, "LDS");
 static_assert(A_BYTES == OUT_STAGE, "out stage 0 reuses the A region");
-static_assert(2 * 2 * BM * 4 <= OUT_STAGE, "row statistics fit in out stage 1");
+static_assert(2 * 4 * BM * 4 <= OUT_STAGE, "row statistics fit in out stage 1");
 
 // Byte offset of 16-byte chunk c (columns 8c .. 8c+7) of row r in an out
 // stage: 256 bytes per row, chunks XOR-swizzled by r % 16, so that the 16
@@ -111,9 +114,9 @@ chain_rows_kernel(const ChainParams p) {
   //           out stage (it-1) & 1 (written in step it-1 for tile it-2,
   //           stored from in I/O step it-1);
   //   BM      between B(nT) and B(nT+1): the pass-1 statistics in LDS.
-  if (wave_u >= 4) {
+  if (wave_u >= NCW) {
     // =========================== I/O waves ===================================
-    const int v = wave_u - 4;
+    const int v = wave_u - NCW;
     const uint32_t lda = (uint32_t)p.lda_bytes, ldb = (uint32_t)p.ldb_bytes;
     {
       // A: the row block (128 rows x K) into LDS once, as A_KT k-tiles of 64
@@ -150,7 +153,7 @@ chain_rows_kernel(const ChainParams p) {
       dma16(rbv, col < N ? off : kOutOfRange, lds0 + (it % S) * STAGE + dma_block(v, q, BPW) * 1024);
     };
     // Stores of stream tile it2 (pass 2, column tile it2 - nT) from out
-    // stage it2 & 1: rows v*32 + 4q + lane/16, chunk lane % 16.
+    // stage it2 & 1: rows v*32 + 4q + lane/16, 16-byte chunk lane % 16.
     auto store_tile = [&](int it2) {
       const uint8_t* os = smem + ((it2 & 1) ? OUT1 : OUT0);
       const int c = lane & 15;
@@ -161,7 +164,8 @@ chain_rows_kernel(const ChainParams p) {
         const u32x4 x = *reinterpret_cast<const u32x4*>(os + out_offset(r, c));
         const uint32_t row = row0 + (uint32_t)r;
         const uint32_t off = min(row, M) * ldo + col * OSZ;  // rows past M: past the descriptor
-        __builtin_amdgcn_raw_buffer_store_b128(x, ro, col < N ? (int)off : (int)kOutOfRange, 0, 0);
+        // non-temporal: whole lines, written once and not read back here
+        __builtin_amdgcn_raw_buffer_store_b128(x, ro, col < N ? (int)off : (int)kOutOfRange, 0, kCachePolicyNT);
       }
     };
     // I/O step `it` (between B(it) and B(it+1)): the loads of tile it+S-1,
@@ -208,8 +212,12 @@ chain_rows_kernel(const ChainParams p) {
   }
 
   // ============================= compute waves ===============================
-  const int wm = wave_u >> 1, wn = wave_u & 1;
-  const int nw = wn * 64;
+  // Compute wave (wm, wn) owns rows wm*64 .. +63 and columns wn*32 .. +31 of
+  // each tile: m-subtiles mt = 0, 1 of 32 x 32.  Waves w and w + 4 share a
+  // SIMD, so that one issues its softmax arithmetic while the other's MFMAs
+  // run (a wave issues VALU work well below the SIMD's rate on its own).
+  const int wm = wave_u >> 2, wn = wave_u & 3;
+  const int nw = wn * 32;
   const int jr = acc_j(lane);
 
   // A fragment of m-subtile mt, k-step s: row wm*64 + mt*32 + lane%32,
@@ -218,10 +226,10 @@ chain_rows_kernel(const ChainParams p) {
     return *reinterpret_cast<const u32x4*>(
         smem + (s / 4) * (BM * 128) + a_lds_offset(wm * 64 + mt * 32 + frag_row(lane), frag_chunk(lane, s % 4)));
   };
-  // B fragment of k-step s of the tile in stage `st`: columns nw + 32 nt .. +31.
-  auto read_b = [&](const uint8_t* st, int s, int nt) {
-    const u32x2 lo = tr_read(st + btr_offset(btr_k(s, 0, lane), btr_n(nw + 32 * nt, lane)));
-    const u32x2 hi = tr_read(st + btr_offset(btr_k(s, 1, lane), btr_n(nw + 32 * nt, lane)));
+  // B fragment of k-step s of the tile in stage `st`: columns nw .. nw+31.
+  auto read_b = [&](const uint8_t* st, int s) {
+    const u32x2 lo = tr_read(st + btr_offset(btr_k(s, 0, lane), btr_n(nw, lane)));
+    const u32x2 hi = tr_read(st + btr_offset(btr_k(s, 1, lane), btr_n(nw, lane)));
     return u32x4{lo[0], lo[1], hi[0], hi[1]};
   };
   const float c2 = p.c2;
@@ -233,11 +241,9 @@ chain_rows_kernel(const ChainParams p) {
     // running statistics (log2 domain) of the lane's two rows over its columns
     float rm[2] = {-INFINITY, -INFINITY}, rs[2] = {0.0f, 0.0f};
     float gsub[2] = {0.0f, 0.0f};  // pass 2: row max + log2(row sum)
-    float nbase[2] = {0.0f, 0.0f}, nmax[2] = {0.0f, 0.0f};
-    float ps[2][4];
-    // One accumulator per 32 x 32 subtile i: m-subtile i & 1, n-subtile i >> 1
-    // (so subtiles 0, 1 share their B fragments, and 2, 3).
-    f32x16 ACC[4];
+    float nbase[2] = {0.0f, 0.0f};  // the exponentials' base of the tile being summed
+    float ps[2];                    // its running sum, being extended
+    f32x16 ACC[2];  // one accumulator per m-subtile
     asm volatile("s_barrier" ::: "memory");  // BA
     // The row block's A fragments (both m-subtiles, all k-steps: 64 VGPRs)
     // are read from LDS once and kept in registers for both passes.
@@ -248,60 +254,53 @@ chain_rows_kernel(const ChainParams p) {
       areg[1][s] = read_a(1, s);
     }
 
-    // ---- epilogue slice q (0..3) of subtile I of stream tile x -------------
-    // EP 1 / 2: pass-1 statistics of a full / ragged tile.  The first
-    // subtile of an m-subtile (nt = 0) takes the tile maximum over both of
-    // its n-subtiles in slice 0 and its exponentials in slices 1, 2; the
-    // second (nt = 1) its exponentials in slices 0..3, then folds them into
-    // the running sum.  EP 3: pass-2 outputs exp2(y - max - log2 sum), four
+    // ---- epilogue slice q (0..3) of m-subtile MT of stream tile x ----------
+    // EP 1 / 2: pass-1 statistics of a full / ragged tile: the tile maximum
+    // and the rescaled running sum in slice 0, the exponentials added in
+    // slices 1, 2, the sum kept in slice 3.  EP 3: pass-2 outputs exp2(y - max - log2 sum), four
     // columns per slice; 16-bit outputs are packed, traded with lane ^ 32
-    // into 16-byte runs and written to out stage x & 1 (subtile 0's runs are
-    // held in registers and written in the next step, so that all of a
+    // into 16-byte runs and written to out stage x & 1 (m-subtile 0's runs
+    // are held in registers and written in the next step, so that all of a
     // tile's writes fall in one step); f32 outputs are stored directly.
     uint32_t pw[8], hold[8];
-    auto epi = [&](auto ep_c, auto i_c, auto q_c, int x) {
+    auto epi = [&](auto ep_c, auto mt_c, auto q_c, int x) {
       constexpr int EP = decltype(ep_c)::value;
-      constexpr int I = decltype(i_c)::value;
+      constexpr int MT = decltype(mt_c)::value;
       constexpr int Q = decltype(q_c)::value;
-      constexpr int mt = I & 1, nt = I >> 1;
       if constexpr (EP == 1 || EP == 2) {
         constexpr bool FULL = EP == 1;
-        const int nvalid = (int)N - x * BN;
-        auto valid = [&](int n2, int v) { return FULL || nw + 32 * n2 + acc_i(lane, v) < nvalid; };
-        if constexpr (nt == 0 && Q == 0) {
+        // column nw + acc_i(lane, v) of the tile is valid when the lane-free
+        // part of acc_i is below lim (one register, not one per v)
+        const int lim = (int)N - x * BN - nw - 4 * (lane >> 5);
+        auto valid = [&](int v) { return FULL || acc_i(0, v) < lim; };
+        if constexpr (Q == 0) {
           float mx = NEG ? INFINITY : -INFINITY;
 #pragma unroll
-          for (int n2 = 0; n2 < 2; ++n2)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-              const float y = valid(n2, v) ? ACC[mt + 2 * n2][v] : mx;
-              mx = NEG ? fminf(mx, y) : fmaxf(mx, y);
-            }
+          for (int v = 0; v < 16; ++v) {
+            const float y = valid(v) ? ACC[MT][v] : mx;
+            mx = NEG ? fminf(mx, y) : fmaxf(mx, y);
+          }
           mx = NEG ? xor32_min(mx) : xor32_max(mx);
           const float tm = FULL ? mx * c2 : (mx == (NEG ? INFINITY : -INFINITY) ? -INFINITY : mx * c2);
-          nmax[mt] = fmaxf(rm[mt], tm);
-          nbase[mt] = FULL ? nmax[mt] : (nmax[mt] == -INFINITY ? 0.0f : nmax[mt]);  // all masked so far
-          ps[mt][0] = rs[mt] * __builtin_amdgcn_exp2f(rm[mt] - nbase[mt]);
-          ps[mt][1] = ps[mt][2] = ps[mt][3] = 0.0f;
-        } else {
-          constexpr int V0 = nt == 0 ? 8 * (Q - 1) : 4 * Q;
-          constexpr int NV = nt == 0 ? 8 : 4;
+          const float nm = fmaxf(rm[MT], tm);
+          nbase[MT] = FULL ? nm : (nm == -INFINITY ? 0.0f : nm);  // all masked so far
+          ps[MT] = rs[MT] * __builtin_amdgcn_exp2f(rm[MT] - nbase[MT]);
+          rm[MT] = nm;
+        } else if constexpr (Q < 3) {
 #pragma unroll
-          for (int v = V0; v < V0 + NV; ++v) {
-            const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(ACC[I][v], c2, -nbase[mt]));
-            ps[mt][v & 3] += valid(nt, v) ? e : 0.0f;
+          for (int v = 8 * (Q - 1); v < 8 * Q; ++v) {
+            const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(ACC[MT][v], c2, -nbase[MT]));
+            ps[MT] += valid(v) ? e : 0.0f;
           }
-          if constexpr (nt == 1 && Q == 3) {
-            rm[mt] = nmax[mt];
-            rs[mt] = (ps[mt][0] + ps[mt][1]) + (ps[mt][2] + ps[mt][3]);
-          }
+        } else {
+          rs[MT] = ps[MT];
         }
       } else if constexpr (EP == 3) {
-        const int r = wm * 64 + mt * 32 + jr;  // row in the block
+        const int r = wm * 64 + MT * 32 + jr;  // row in the block
         float po[4];
 #pragma unroll
         for (int v = 0; v < 4; ++v)
-          po[v] = __builtin_amdgcn_exp2f(__builtin_fmaf(ACC[I][4 * Q + v], c2, -gsub[mt]));
+          po[v] = __builtin_amdgcn_exp2f(__builtin_fmaf(ACC[MT][4 * Q + v], c2, -gsub[MT]));
         if constexpr (STAGED) {
           pack4<OUT_DT>(f32x4{po[0], po[1], po[2], po[3]}, &pw[2 * Q], &pw[2 * Q + 1]);
           if constexpr (Q == 3) {
@@ -317,7 +316,7 @@ chain_rows_kernel(const ChainParams p) {
             const auto q3 = __builtin_amdgcn_permlane32_swap(pw[5], pw[7], false, false);
             const u32x4 run0 = u32x4{q0[0], q1[0], q0[1], q1[1]};
             const u32x4 run1 = u32x4{q2[0], q3[0], q2[1], q3[1]};
-            if constexpr (I == 0) {
+            if constexpr (MT == 0) {
 #pragma unroll
               for (int w = 0; w < 4; ++w) {
                 hold[w] = run0[w];
@@ -325,7 +324,7 @@ chain_rows_kernel(const ChainParams p) {
               }
             } else {
               uint8_t* os = smem + ((x & 1) ? OUT1 : OUT0);
-              const int c0 = wn * 8 + nt * 4 + (lane >> 5);  // chunk of run 0; run 1 is c0 + 2
+              const int c0 = wn * 4 + (lane >> 5);  // chunk of run 0; run 1 is c0 + 2
               *reinterpret_cast<u32x4*>(os + out_offset(r, c0)) = run0;
               *reinterpret_cast<u32x4*>(os + out_offset(r, c0 + 2)) = run1;
             }
@@ -333,30 +332,31 @@ chain_rows_kernel(const ChainParams p) {
         } else {
           // f32: lane l < 32 holds columns 8Q + 0..3, lane l + 32 columns 8Q + 4..7
           const uint32_t row = row0 + (uint32_t)r;
-          const uint32_t col = (uint32_t)(x - nT) * BN + nw + 32 * nt + 8 * Q + 4 * (lane >> 5);
+          const uint32_t col = (uint32_t)(x - nT) * BN + nw + 8 * Q + 4 * (lane >> 5);
           const uint32_t off = min(row, M) * ldo + col * 4;  // rows past M: past the descriptor
           __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, f32x4{po[0], po[1], po[2], po[3]}),
                                                  ro, col < N ? (int)off : (int)kOutOfRange, 0, 0);
         }
       }
     };
-    // subtile 0's held runs of stream tile x into out stage x & 1
+    // m-subtile 0's held runs of stream tile x into out stage x & 1
     auto write_hold = [&](int x) {
       uint8_t* os = smem + ((x & 1) ? OUT1 : OUT0);
       const int r = wm * 64 + jr;
-      const int c0 = wn * 8 + (lane >> 5);
+      const int c0 = wn * 4 + (lane >> 5);
       *reinterpret_cast<u32x4*>(os + out_offset(r, c0)) = u32x4{hold[0], hold[1], hold[2], hold[3]};
       *reinterpret_cast<u32x4*>(os + out_offset(r, c0 + 2)) = u32x4{hold[4], hold[5], hold[6], hold[7]};
     };
 
-    // Step `it`, in 4 phases after barrier B(it).  Phase ph (1..4) runs the 8
-    // MFMAs of subtile ph-1 of tile it (MMA) beside the epilogue of subtile
-    // ph & 3: of tile it-1 (EPA) in phases 1..3, of tile it (EPB) in phase 4
-    // -- each epilogue reads an accumulator that no MFMA of its phase writes,
-    // and every subtile it needs is complete.  Each phase is 4 groups of two
-    // MFMAs and one epilogue slice, so the matrix core runs while the wave
-    // issues the slice.  MERGE: the pass-1 statistics of the two column-waves
-    // are merged after phase 3 (tile it-1 = nT-1 is then complete).
+    // Step `it`, in 2 phases after barrier B(it): phase 1 runs the 8 MFMAs
+    // of m-subtile 0 of tile it beside the epilogue of m-subtile 1 of tile
+    // it-1 (EPA), phase 2 the MFMAs of m-subtile 1 of tile it beside the
+    // epilogue of m-subtile 0 of tile it (EPB) -- each epilogue reads an
+    // accumulator that no MFMA of its phase writes.  The step's 8 B
+    // fragments serve both phases.  Each phase is 4 groups of two MFMAs and
+    // one epilogue slice, so the matrix core runs while the wave issues the
+    // slice.  MERGE: the pass-1 statistics of the four column-waves are
+    // merged after phase 1 (tile it-1 = nT-1 is then complete).
     auto step = [&](auto epa_c, auto epb_c, auto mma_c, auto merge_c, int it) {
       constexpr int EPA = decltype(epa_c)::value;
       constexpr int EPB = decltype(epb_c)::value;
@@ -366,18 +366,18 @@ chain_rows_kernel(const ChainParams p) {
       asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // B(it)
       __builtin_amdgcn_sched_barrier(0);
       const uint8_t* st = smem + RING_OFF + (it % S) * STAGE;
-      u32x4 bf[2][KS];
+      u32x4 bf[KS];
       if constexpr (MMA) {
 #pragma unroll
-        for (int s = 0; s < KS; ++s) bf[0][s] = read_b(st, s, 0);
+        for (int s = 0; s < KS; ++s) bf[s] = read_b(st, s);
       }
       if constexpr (EPA == 3 && STAGED) write_hold(it - 1);
       auto phase = [&](auto ph_c) {
         constexpr int PH = decltype(ph_c)::value;
-        constexpr int I = PH - 1;   // MFMA subtile
-        constexpr int EI = PH & 3;  // epilogue subtile
-        constexpr int EP = PH < 4 ? EPA : EPB;
-        const int x = PH < 4 ? it - 1 : it;
+        constexpr int I = PH - 1;   // m-subtile of the MFMAs
+        constexpr int EI = PH & 1;  // m-subtile of the epilogue
+        constexpr int EP = PH == 1 ? EPA : EPB;
+        const int x = PH == 1 ? it - 1 : it;
         auto group = [&](auto q_c) {
           constexpr int Q = decltype(q_c)::value;
           if constexpr (MMA) {
@@ -388,14 +388,13 @@ chain_rows_kernel(const ChainParams p) {
                   f32x16 z;
 #pragma unroll
                   for (int v = 0; v < 16; ++v) z[v] = 0.0f;
-                  ACC[I] = mfma16<IN_DT>(bf[I >> 1][s], areg[I & 1][s], z);
+                  ACC[I] = mfma16<IN_DT>(bf[s], areg[I][s], z);
                 } else {
-                  ACC[I] = mfma16<IN_DT>(bf[I >> 1][s], areg[I & 1][s], ACC[I]);
+                  ACC[I] = mfma16<IN_DT>(bf[s], areg[I][s], ACC[I]);
                 }
               } else {
-                ACC[I] = mfma16<IN_DT>(bf[I >> 1][s], areg[I & 1][s], ACC[I]);
+                ACC[I] = mfma16<IN_DT>(bf[s], areg[I][s], ACC[I]);
               }
-              if constexpr (PH == 2) bf[1][s] = read_b(st, s, 1);
             }
           }
           if constexpr (EP != 0) epi(std::integral_constant<int, EP>{}, std::integral_constant<int, EI>{}, q_c, x);
@@ -407,13 +406,11 @@ chain_rows_kernel(const ChainParams p) {
         group(std::integral_constant<int, 3>{});
       };
       phase(std::integral_constant<int, 1>{});
-      phase(std::integral_constant<int, 2>{});
-      phase(std::integral_constant<int, 3>{});
       if constexpr (MERGE) {
-        // BM: merge the 2 column-waves of each row through out stage 1,
+        // BM: merge the 4 column-waves of each row through out stage 1,
         // which holds no output before step nT + 1.
-        float* redmax = reinterpret_cast<float*>(smem + OUT1);  // [2][BM]
-        float* redsum = redmax + 2 * BM;                        // [2][BM]
+        float* redmax = reinterpret_cast<float*>(smem + OUT1);  // [4][BM]
+        float* redsum = redmax + 4 * BM;                        // [4][BM]
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
           const float sum = xor32_sum(rs[mt]);
@@ -426,15 +423,20 @@ chain_rows_kernel(const ChainParams p) {
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
           const int row = wm * 64 + mt * 32 + jr;
-          const float m0 = redmax[row], m1 = redmax[BM + row];
-          const float gm = fmaxf(m0, m1);
-          const float gs = (m0 == -INFINITY ? 0.0f : redsum[row] * __builtin_amdgcn_exp2f(m0 - gm)) +
-                           (m1 == -INFINITY ? 0.0f : redsum[BM + row] * __builtin_amdgcn_exp2f(m1 - gm));
+          float gm = redmax[row];
+#pragma unroll
+          for (int w = 1; w < 4; ++w) gm = fmaxf(gm, redmax[w * BM + row]);
+          float gs = 0.0f;
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            const float mw = redmax[w * BM + row];
+            gs += mw == -INFINITY ? 0.0f : redsum[w * BM + row] * __builtin_amdgcn_exp2f(mw - gm);
+          }
           gsub[mt] = gm + __builtin_amdgcn_logf(gs);  // v_log_f32 is log2
         }
         __builtin_amdgcn_sched_barrier(0);
       }
-      phase(std::integral_constant<int, 4>{});
+      phase(std::integral_constant<int, 2>{});
     };
     using Y = std::true_type;
     using F = std::false_type;
