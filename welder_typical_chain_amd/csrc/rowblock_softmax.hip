@@ -353,10 +353,11 @@ chain_rows_kernel(const ChainParams p) {
     // it-1 (EPA), phase 2 the MFMAs of m-subtile 1 of tile it beside the
     // epilogue of m-subtile 0 of tile it (EPB) -- each epilogue reads an
     // accumulator that no MFMA of its phase writes.  The step's 8 B
-    // fragments serve both phases.  Each phase is 4 groups of two MFMAs and
-    // one epilogue slice, so the matrix core runs while the wave issues the
-    // slice.  MERGE: the pass-1 statistics of the four column-waves are
-    // merged after phase 1 (tile it-1 = nT-1 is then complete).
+    // fragments serve both phases.  Phase 2 is 4 groups of two MFMAs and one
+    // epilogue slice, so the matrix core runs while the wave issues the
+    // slice; phase 1 issues its epilogue before its MFMAs.  MERGE: the
+    // pass-1 statistics of the four column-waves are merged after phase 1
+    // (tile it-1 = nT-1 is then complete).
     auto step = [&](auto epa_c, auto epb_c, auto mma_c, auto merge_c, int it) {
       constexpr int EPA = decltype(epa_c)::value;
       constexpr int EPB = decltype(epb_c)::value;
@@ -380,6 +381,16 @@ chain_rows_kernel(const ChainParams p) {
         const int x = PH == 1 ? it - 1 : it;
         auto group = [&](auto q_c) {
           constexpr int Q = decltype(q_c)::value;
+          // Phase 1: the whole epilogue first, while the step's B fragment
+          // reads are in flight (an MFMA that waits for its fragment holds
+          // up the instructions behind it).
+          if constexpr (PH == 1 && Q == 0 && EP != 0) {
+            epi(std::integral_constant<int, EP>{}, std::integral_constant<int, EI>{}, std::integral_constant<int, 0>{}, x);
+            epi(std::integral_constant<int, EP>{}, std::integral_constant<int, EI>{}, std::integral_constant<int, 1>{}, x);
+            epi(std::integral_constant<int, EP>{}, std::integral_constant<int, EI>{}, std::integral_constant<int, 2>{}, x);
+            epi(std::integral_constant<int, EP>{}, std::integral_constant<int, EI>{}, std::integral_constant<int, 3>{}, x);
+            __builtin_amdgcn_sched_barrier(0);
+          }
           if constexpr (MMA) {
 #pragma unroll
             for (int s = 2 * Q; s < 2 * Q + 2; ++s) {
@@ -397,7 +408,7 @@ chain_rows_kernel(const ChainParams p) {
               }
             }
           }
-          if constexpr (EP != 0) epi(std::integral_constant<int, EP>{}, std::integral_constant<int, EI>{}, q_c, x);
+          if constexpr (PH == 2 && EP != 0) epi(std::integral_constant<int, EP>{}, std::integral_constant<int, EI>{}, q_c, x);
           __builtin_amdgcn_sched_barrier(0);
         };
         group(std::integral_constant<int, 0>{});
