@@ -10,7 +10,9 @@
 // small integers so the products are exact; the result must equal the plain
 // integer matmul.  Also checks that every LDS byte of the stage is written
 // exactly once, that the XCD remap is a bijection, and counts LDS bank
-// conflicts (64 banks x 4 bytes, 16 lanes per 128-bit access phase).
+// conflicts (64 banks x 4 bytes, 16 lanes per 128-bit access phase).  Also
+// replays the row-block kernel's pass-2 output hand-off through its LDS out
+// stage (run_rows_out).
 //
 // Build: g++ -O2 -std=c++17 -I<csrc> layout_check.cpp; prints "OK" and exits 0.
 #include <cstdint>
@@ -442,7 +444,84 @@ static void run_wide(int sz) {
   CHECK(ca.worst == 1 && cb.worst == 1, "[%s] fragment reads conflict\n", name);
 }
 
+
+// The row-block kernel's pass-2 hand-off of a 128x128 tile of 16-bit outputs
+// (chain_rows_kernel): compute wave (wm, wn) holds, per m-subtile mt, the
+// 16 values of row l % 32 its lane l keeps in the accumulator layout
+// (register v: column acc_i(l, v) of its 32 columns), packs them in pairs
+// into 8 words, trades halves with lane l ^ 32 (v_permlane32_swap of words
+// w and w + 2 leaves {x[0..31], y[0..31]} in x and {x[32..63], y[32..63]} in
+// y) and writes two 16-byte runs at rows_out_offset(row, wn*4 + l/32 + 2h);
+// I/O wave v reads row v*32 + 4q + l/16, chunk l % 16, and stores it at
+// columns 8 (l % 16) .. +7.  Checks that every read finds its row's 8
+// columns in order, that every 16-byte slot is written exactly once, and
+// counts bank conflicts of both sides.
+static void run_rows_out() {
+  struct Word { int row, col0, col1; };
+  std::vector<std::vector<Word>> lds(128 * 16);  // 16-byte slots: 4 words
+  std::vector<int> writes(128 * 16, 0);
+  Conflicts cw, cr;
+  for (int wm = 0; wm < 2; ++wm)
+    for (int wn = 0; wn < 4; ++wn)
+      for (int mt = 0; mt < 2; ++mt) {
+        Word pw[64][8];
+        for (int l = 0; l < 64; ++l)
+          for (int g = 0; g < 4; ++g)
+            for (int h = 0; h < 2; ++h)
+              pw[l][2 * g + h] = {wm * 64 + mt * 32 + l % 32, wn * 32 + acc_i(l, 4 * g + 2 * h),
+                                  wn * 32 + acc_i(l, 4 * g + 2 * h + 1)};
+        // q[i][0/1][l]: v_permlane32_swap(pw[a], pw[b]) for (a, b) = (0,2) (1,3) (4,6) (5,7)
+        const int ab[4][2] = {{0, 2}, {1, 3}, {4, 6}, {5, 7}};
+        Word q[4][2][64];
+        for (int i = 0; i < 4; ++i)
+          for (int l = 0; l < 64; ++l) {
+            q[i][0][l] = l < 32 ? pw[l][ab[i][0]] : pw[l - 32][ab[i][1]];
+            q[i][1][l] = l < 32 ? pw[l + 32][ab[i][0]] : pw[l][ab[i][1]];
+          }
+        for (int h = 0; h < 2; ++h) {
+          std::vector<int> addrs;
+          for (int l = 0; l < 64; ++l) {
+            const int i0 = 2 * h, i1 = 2 * h + 1;
+            const std::vector<Word> run = {q[i0][0][l], q[i1][0][l], q[i0][1][l], q[i1][1][l]};
+            const int row = wm * 64 + mt * 32 + l % 32, chunk = wn * 4 + l / 32 + 2 * h;
+            const int off = rows_out_offset(row, chunk);
+            CHECK(off >= 0 && off % 16 == 0 && off < 128 * 256, "rows out: offset %d out of the stage\n", off);
+            lds[off / 16] = run;
+            writes[off / 16]++;
+            addrs.push_back(off);
+            if (addrs.size() == 16) {
+              cw.phase(addrs, 16);
+              addrs.clear();
+            }
+          }
+        }
+      }
+  for (int sl = 0; sl < 128 * 16; ++sl) CHECK(writes[sl] == 1, "rows out: slot %d written %d times\n", sl, writes[sl]);
+  for (int v = 0; v < 4; ++v)
+    for (int qq = 0; qq < 8; ++qq) {
+      std::vector<int> addrs;
+      for (int l = 0; l < 64; ++l) {
+        const int r = v * 32 + 4 * qq + l / 16, c = l % 16;
+        const int off = rows_out_offset(r, c);
+        const std::vector<Word>& run = lds[off / 16];
+        CHECK(run.size() == 4, "rows out: empty slot read\n");
+        for (int w = 0; w < (int)run.size(); ++w)
+          CHECK(run[w].row == r && run[w].col0 == 8 * c + 2 * w && run[w].col1 == 8 * c + 2 * w + 1,
+                "rows out: row %d chunk %d word %d holds row %d columns %d,%d\n", r, c, w, run[w].row,
+                run[w].col0, run[w].col1);
+        addrs.push_back(off);
+        if (addrs.size() == 16) {
+          cr.phase(addrs, 16);
+          addrs.clear();
+        }
+      }
+    }
+  std::printf("rows out stage: bank conflict degree write %d read %d\n", cw.worst, cr.worst);
+  CHECK(cw.worst == 1 && cr.worst == 1, "rows out: bank conflicts\n");
+}
+
 int main() {
+  run_rows_out();
   run_dma16();
   run_dma8();
   run_wide(2);

@@ -65,11 +65,8 @@ static_assert(LDS_BYTES <= 160 * 1024, "LDS");
 static_assert(A_BYTES == OUT_STAGE, "out stage 0 reuses the A region");
 static_assert(2 * 4 * BM * 4 <= OUT_STAGE, "row statistics fit in out stage 1");
 
-// Byte offset of 16-byte chunk c (columns 8c .. 8c+7) of row r in an out
-// stage: 256 bytes per row, chunks XOR-swizzled by r % 16, so that the 16
-// rows of a compute wave's store and the 16 chunks of an I/O wave's row
-// both fall in 16 distinct bank groups.
-__device__ inline int out_offset(int r, int c) { return r * 256 + ((c ^ (r & 15)) << 4); }
+// the out stage's layout: rows_out_offset (tile_layout.h)
+__device__ inline int out_offset(int r, int c) { return rows_out_offset(r, c); }
 
 }  // namespace rows
 

@@ -221,4 +221,11 @@ WTC_HD void tile_of_block(uint32_t b, uint32_t G, uint32_t rows, uint32_t cols, 
   *col = r / in_group;
 }
 
+// ---- the row-block kernel's output stage (16-bit outputs) ----------------
+// Byte offset of 16-byte chunk c (columns 8c .. 8c+7) of row r in an out
+// stage of 128-column tiles: 256 bytes per row, chunks XOR-swizzled by
+// r % 16, so that the 16 rows of a compute wave's 16-byte write and the 16
+// chunks of an I/O wave's row read both fall in 16 distinct bank groups.
+WTC_HD constexpr int rows_out_offset(int r, int c) { return r * 256 + ((c ^ (r & 15)) << 4); }
+
 } // namespace wtc
